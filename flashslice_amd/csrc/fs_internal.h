@@ -1,0 +1,66 @@
+// Internal launch interface between the C-ABI (fs_abi.cpp) and the kernel
+// translation units. Not part of the public C-ABI (include/flashslice_hip.h).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fs {
+
+enum DType { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
+
+// One launch's operands. Point tensors (B, N, H, C) are read and written
+// through element strides along b, n, h with unit stride along the last
+// dim. Small tensors are fp32 and contiguous; weight and bias carry the
+// element strides along b and h that are zero where the tensor is shared
+// (reference slice_ops.py:461-478).
+struct Args {
+  const void* x;  int64_t sxb, sxn, sxh;   // x_mid (B, N, H, D)
+  const void* f;  int64_t sfb, sfn, sfh;   // fx_mid or d_out (B, N, H, DV)
+  void* o1;       int64_t s1b, s1n, s1h;   // out (deslice fwd) or dx (bwd)
+  void* o2;       int64_t s2b, s2n, s2h;   // dfx (slice bwd)
+  const float* W;    int64_t swb, swh;     // (.., G, D)
+  const float* bias; int64_t sbb, sbh;     // (.., G)
+  const float* tau;                        // (H,)
+  const float* tok;                        // (B, H, G, DV): tokens or dz_num
+  const float* ds;                         // (B, H, G): d s (slice bwd)
+  const float* stats_in;                   // (B, H, 2, N) or null
+  float* stats_out;                        // (B, H, 2, N) or null
+  float* delta;                            // (B, H, N) scratch (blocked bwd)
+  float* part;                             // per-wave partials (workspace)
+  int B, N, H, D, DV, G;
+  int P;                                   // point partitions per (b, h)
+  int ntiles;                              // ceil(N / 32)
+  int vec_x, vec_f, vec_1, vec_2;          // 4-element alignment of rows
+  int nblk;                                // slot blocks held per wave (blocked family)
+};
+
+// Partial-buffer layout of one wave (floats), fused family:
+//   slice fwd:   z [G][DV], s [G]
+//   slice bwd:   dW [G][D], db [G], dtau [1]
+//   deslice bwd: dtok [G][DV], dW [G][D], db [G], dtau [1]
+__host__ __device__ inline int64_t part_floats_slice_fwd(int G, int DV) { return (int64_t)G * DV + G; }
+__host__ __device__ inline int64_t part_floats_slice_bwd(int G, int D) { return (int64_t)G * D + G + 1; }
+__host__ __device__ inline int64_t part_floats_deslice_bwd(int G, int D, int DV) {
+  return (int64_t)G * DV + (int64_t)G * D + G + 1;
+}
+
+constexpr int kWavesPerBlock = 4;
+constexpr int kTile = 32;               // points per wave tile
+
+// fused (whole G in registers) family; returns hipSuccess or an error
+hipError_t launch_fused_slice_fwd(const Args& a, int dtype, int mode, hipStream_t st);
+hipError_t launch_fused_deslice_fwd(const Args& a, int dtype, int mode, hipStream_t st);
+hipError_t launch_fused_slice_bwd(const Args& a, int dtype, int mode, hipStream_t st);
+hipError_t launch_fused_deslice_bwd(const Args& a, int dtype, int mode, hipStream_t st);
+bool fused_fits(int D, int DV, int G);
+
+// deterministic reductions of per-wave partials
+// out[ob][oh][e] = scale * sum_{b -> ob} sum_{h -> oh} sum_{p < P} part[(b*H+h)*P + p][off + e]
+// where b maps to ob = (Bo > 1 ? b : 0) and h to oh = (Ho > 1 ? h : 0).
+hipError_t launch_reduce_parts(const float* part, int64_t wave_stride, int64_t off, int E, int B,
+                               int H, int P, int Bo, int Ho, float* out, hipStream_t st);
+// dtau[h] = sum_b sum_p part[(b*H+h)*P + p][off]
+hipError_t launch_reduce_scalar(const float* part, int64_t wave_stride, int64_t off, int B, int H,
+                                int P, float* out, hipStream_t st);
+
+}  // namespace fs

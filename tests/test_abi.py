@@ -1,0 +1,125 @@
+"""The C ABI library (CPU-only checks: no kernel is launched).
+
+* the in-tree library loads and exports every entry point that
+  ``include/flashslice_hip.h`` declares;
+* argument validation happens before any launch and reports through
+  ``fs_last_error`` (these calls never reach the GPU);
+* workspace sizing and family routing are pure functions of the shape.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from flashslice_amd.kernels import _hip
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "flashslice_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(fs_[a-z_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _hip.lib()
+    names = _declared()
+    assert set(names) == set(_hip.EXPORTS), names
+    for n in names:
+        assert hasattr(lib, n), n
+    assert b"gfx950" in lib.fs_version()
+
+
+def test_nm_lists_the_symbols():
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", _hip.LIB_PATH],
+                         capture_output=True, text=True).stdout
+    for n in _declared():
+        assert re.search(r"\bT %s$" % n, out, re.M), n
+
+
+def _params(B=1, N=100, H=2, D=32, DV=32, G=32, dot=0):
+    w = torch.zeros(G, D)
+    b = torch.zeros(G)
+    tau = torch.ones(H)
+    p = _hip.FsSliceParams(B, N, H, D, DV, G, w.data_ptr(), 0, 0, b.data_ptr(), 0, 0,
+                           tau.data_ptr(), dot, 0)
+    return p, (w, b, tau)
+
+
+def test_validation_before_launch():
+    lib = _hip.lib()
+    p, keep = _params()
+    x = _hip.FsPoints(None, 0, 0, 0, 0, 32)
+    rc = lib.fs_slice_fwd(ctypes.byref(x), ctypes.byref(x), ctypes.byref(p), None, None,
+                          None, None, None, 0, None)
+    assert rc == _hip.FS_ERR_INVALID
+    assert b"x_mid is NULL" in lib.fs_last_error()
+    bad, keep2 = _params(D=300)
+    rc = lib.fs_deslice_fwd(ctypes.byref(x), ctypes.byref(bad), None, None, None,
+                            ctypes.byref(x), None, 0, None)
+    assert rc == _hip.FS_ERR_INVALID and b"[1, 256]" in lib.fs_last_error()
+    bad, keep3 = _params(G=0)
+    rc = lib.fs_slice_bwd(ctypes.byref(x), ctypes.byref(x), ctypes.byref(bad), None, None,
+                          None, ctypes.byref(x), ctypes.byref(x), None, None, None, None, 0,
+                          None)
+    assert rc == _hip.FS_ERR_INVALID and b"G must be" in lib.fs_last_error()
+    bad, keep4 = _params(dot=7)
+    rc = lib.fs_deslice_bwd(ctypes.byref(x), ctypes.byref(bad), None, None, ctypes.byref(x),
+                            ctypes.byref(x), None, None, None, None, None, 0, None)
+    assert rc == _hip.FS_ERR_INVALID and b"dot level" in lib.fs_last_error()
+
+
+def test_dtype_and_width_mismatch_rejected():
+    lib = _hip.lib()
+    p, keep = _params()
+    buf = torch.zeros(16)
+    x = _hip.FsPoints(buf.data_ptr(), 0, 0, 0, 0, 32)
+    fx = _hip.FsPoints(buf.data_ptr(), 0, 0, 0, 1, 32)
+    z = ctypes.c_void_p(buf.data_ptr())
+    rc = lib.fs_slice_fwd(ctypes.byref(x), ctypes.byref(fx), ctypes.byref(p), None, None, z, z,
+                          None, 0, None)
+    assert rc == _hip.FS_ERR_INVALID and b"dtypes differ" in lib.fs_last_error()
+    fx = _hip.FsPoints(buf.data_ptr(), 0, 0, 0, 0, 31)
+    rc = lib.fs_slice_fwd(ctypes.byref(x), ctypes.byref(fx), ctypes.byref(p), None, None, z, z,
+                          None, 0, None)
+    assert rc == _hip.FS_ERR_INVALID and b"width 31" in lib.fs_last_error()
+
+
+def test_workspace_too_small_rejected():
+    lib = _hip.lib()
+    p, keep = _params(N=4096)
+    need = lib.fs_workspace_bytes(_hip.OP_SLICE_FWD, ctypes.byref(p))
+    assert need > 0
+    buf = torch.zeros(16)
+    x = _hip.FsPoints(buf.data_ptr(), 0, 0, 0, 0, 32)
+    z = ctypes.c_void_p(buf.data_ptr())
+    rc = lib.fs_slice_fwd(ctypes.byref(x), ctypes.byref(x), ctypes.byref(p), None, None, z, z,
+                          z, need - 4, None)
+    assert rc == _hip.FS_ERR_WORKSPACE and b"workspace" in lib.fs_last_error()
+
+
+@pytest.mark.parametrize("N,B,H,G,DV", [(4096, 1, 8, 32, 32), (1_000_000, 1, 8, 32, 32),
+                                        (262144, 4, 8, 64, 64), (17, 2, 4, 256, 32)])
+def test_workspace_is_a_function_of_the_shape(N, B, H, G, DV):
+    lib = _hip.lib()
+    p, keep = _params(B=B, N=N, H=H, G=G, DV=DV)
+    a = lib.fs_workspace_bytes(_hip.OP_SLICE_BWD, ctypes.byref(p))
+    b = lib.fs_workspace_bytes(_hip.OP_SLICE_BWD, ctypes.byref(p))
+    assert a == b and a % 4 == 0
+    assert lib.fs_workspace_bytes(_hip.OP_DESLICE_FWD, ctypes.byref(p)) == 0
+    # partials are O(B H P G (D+1)), far below the N x H x G tensor at scale
+    if N >= 262144:
+        assert a < B * N * H * G * 4 / 10
+
+
+def test_family_routing():
+    lib = _hip.lib()
+    for (D, DV, G), fam in (((32, 32, 32), 1), ((32, 64, 64), 1), ((32, 32, 128), 1),
+                            ((32, 32, 256), 2), ((32, 32, 1024), 2), ((256, 32, 32), 2)):
+        p, keep = _params(D=D, DV=DV, G=G)
+        assert lib.fs_family(ctypes.byref(p)) == fam, (D, DV, G)
