@@ -1,0 +1,251 @@
+"""Benchmark of the fused slice/deslice hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3-256|c3-1024|c4]
+
+One step is the coupling the metric names ("slice+deslice
+fwd+bwd ms & Mpoints/s at N=1M, H=8, D=32, G=32; peak HBM"): the four
+``torch.ops.flashslice`` operators on one batch of synthetic points already
+resident in HBM, in the order autograd runs them --
+
+    z_num, s   = flash_slice(x, fx, W, b, tau)           slice forward
+    tokens     = z_num / (s + 1e-5)                      (torch, tiny)
+    out        = flash_deslice(x, W, b, tau, tokens)     deslice forward
+    dx1, dtok, dW1, db1, dtau1 = flash_deslice_bwd(..., d_out)
+    dz, ds     = chain rule through tokens               (torch, tiny)
+    dx2, dfx, dW2, db2, dtau2 = flash_slice_bwd(..., dz, ds)
+
+with upstream gradients d_out, dz_num, ds ~ N(0, 1) (the loss of reference
+bench/parity_ops.py:148-151). Inputs follow BASELINE.json config 2: x, fx
+~ N(0, 1) (1, 1e6, 8, 32) fp32; per-head W ~ N(0, 1/D); b ~ N(0, 0.02^2);
+tau ~ U[0.3, 1.0]. ``value`` is points per second of the whole step.
+
+Printed: ONE JSON line with the driver's fields, plus ``roofline`` (the
+dominant kernel's algorithmic bytes per launch over its HIP-event time on
+its stream), ``step_roofline`` (all four ops' algorithmic bytes over the
+step), ``cpu_baseline`` (the CPU oracle -- the eager PyTorch softmax/einsum
+path -- timed on a bounded sample on this host's cores), ``peak_hbm_gb``,
+``per_op_ms`` and ``deterministic``.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, published
+MFMA_F32_TFLOPS = 157.3         # MI355X dense fp32 MFMA, published
+EPS = 1e-5
+
+WORKLOADS = {
+    # name: (B, N, H, D, DV, G, weight layout, description)
+    "c2": (1, 1_000_000, 8, 32, 32, 32, "hgd",
+           "C2: slice->deslice fwd+bwd, B=1 N=1e6 H=8 D=DV=32 G=32 fp32 ieee, per-head W"),
+    "c4": (4, 262_144, 8, 32, 64, 64, "bhgd",
+           "C4: B=4 N=262144 H=8 D=32 DV=64 G=64 fp32, per-sample W"),
+}
+
+
+def make_inputs(B, N, H, D, DV, G, layout, device, seed=0):
+    """Synthetic inputs of BASELINE.json's configs, generated on the CPU from
+    one seed (so the CPU baseline and the GPU see the same values)."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, N, H, D, generator=g)
+    fx = torch.randn(B, N, H, DV, generator=g)
+    wshape = {"gd": (G, D), "hgd": (H, G, D), "bhgd": (B, H, G, D)}[layout]
+    W = torch.randn(*wshape, generator=g) / D ** 0.5
+    b = 0.02 * torch.randn(*wshape[:-1], generator=g)
+    tau = 0.3 + 0.7 * torch.rand(H, generator=g)
+    d_out = torch.randn(B, N, H, DV, generator=g)
+    dzb = torch.randn(B, H, G, DV, generator=g)
+    dsb = torch.randn(B, H, G, generator=g)
+    to = lambda t: t.to(device)  # noqa: E731
+    return tuple(map(to, (x, fx, W, b, tau, d_out, dzb, dsb)))
+
+
+def alg_bytes(B, N, H, D, DV, e=4):
+    """Algorithmic HBM bytes per op (x-sized passes; reference
+    bench/bench_kernels.py:45): slice fwd reads x, fx; deslice fwd reads x,
+    writes out; deslice bwd reads x, d_out, writes dx; slice bwd reads x, fx,
+    writes dx, dfx."""
+    pts = B * N * H
+    return {"slice_fwd": pts * (D + DV) * e, "deslice_fwd": pts * (D + DV) * e,
+            "deslice_bwd": pts * (D + 2 * DV) * e, "slice_bwd": pts * (2 * D + 2 * DV) * e}
+
+
+def alg_flops(B, N, H, D, DV, G):
+    """Algorithmic FLOPs per op (14 dots per step: logits recomputed in each
+    op, 1 value dot per forward, 3 more dots per backward)."""
+    u = 2 * B * N * H * G
+    return {"slice_fwd": u * (D + DV), "deslice_fwd": u * (D + DV),
+            "deslice_bwd": u * (3 * D + 2 * DV),  # logits, dtokens, omega, dx, dW
+            "slice_bwd": u * (3 * D + 2 * DV)}
+
+
+def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, ev=None):
+    ops = torch.ops.flashslice
+
+    def mark(i):
+        if ev is not None:
+            ev[i].record()
+
+    mark(0)
+    z, s = ops.flash_slice(x, fx, W, b, tau, 0)
+    mark(1)
+    den = (s + EPS)[..., None]
+    tok = z / den
+    out = ops.flash_deslice(x, W, b, tau, tok, 0)
+    mark(2)
+    dx1, dtok, dW1, db1, dt1 = ops.flash_deslice_bwd(x, W, b, tau, tok, d_out, 0)
+    mark(3)
+    dz = dzb + dtok / den
+    ds = dsb - (dtok * tok).sum(-1) / den[..., 0]
+    dx2, dfx, dW2, db2, dt2 = ops.flash_slice_bwd(x, fx, W, b, tau, dz, ds, 0)
+    mark(4)
+    return z, s, out, dx1, dtok, dW1, db1, dt1, dx2, dfx, dW2, db2, dt2
+
+
+def cpu_baseline(B, H, D, DV, G, layout, budget_s=20.0):
+    """The eager PyTorch softmax/einsum path (the CPU oracle, fp32) on this
+    host's cores, forward + backward of the same coupling on a bounded
+    sample of points; returns points/s."""
+    import oracle
+    torch.set_num_threads(os.cpu_count() or 1)
+    n = 32768
+    x, fx, W, b, tau, d_out, dzb, dsb = make_inputs(B, n, H, D, DV, G, layout, "cpu")
+
+    def run():
+        leaves = [t.clone().requires_grad_(True) for t in (x, fx, W, b, tau)]
+        out, z, s = oracle.coupling(*leaves, order="slice-first")
+        oracle.coupling_loss(out, z, s, d_out, dzb, dsb).backward()
+
+    run()
+    t0 = time.perf_counter()
+    run()
+    one = time.perf_counter() - t0
+    # grow the sample until one run is ~1/4 of the budget, then time 3 runs
+    while one < budget_s / 8 and n < 1_000_000:
+        n *= 2
+        x, fx, W, b, tau, d_out, dzb, dsb = make_inputs(B, n, H, D, DV, G, layout, "cpu")
+        t0 = time.perf_counter()
+        run()
+        one = time.perf_counter() - t0
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return B * n / ts[1], n, torch.get_num_threads()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    a = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: every GPU box of this build has one, and the "
+              "slice/deslice path is measured on one GPU's share (N=%d requested)" % a.gpus,
+              file=sys.stderr)
+        sys.exit(2)
+
+    import flashslice_amd.kernels  # noqa: F401  -- registers torch.ops.flashslice
+    from flashslice_amd.kernels import _hip
+
+    B, N, H, D, DV, G, layout, desc = WORKLOADS[a.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    inputs = make_inputs(B, N, H, D, DV, G, layout, dev)
+    torch.cuda.synchronize()
+    print("[bench] %s; library %s" % (desc, _hip.lib().fs_version().decode()),
+          file=sys.stderr, flush=True)
+
+    for _ in range(a.warmup):
+        step_ops(*inputs)
+    torch.cuda.synchronize()
+
+    # determinism: two steps bitwise equal
+    r1 = [t.clone() for t in step_ops(*inputs)]
+    r2 = step_ops(*inputs)
+    deterministic = all(torch.equal(u, v) for u, v in zip(r1, r2))
+    del r1, r2
+
+    # peak HBM of one step above the resident inputs
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    res = step_ops(*inputs)
+    torch.cuda.synchronize()
+    peak_gb = (torch.cuda.max_memory_allocated() - base) / 1e9
+    del res
+
+    # timed region: K steps, per-op HIP events on the launch stream
+    stream = torch.cuda.current_stream()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(a.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(a.steps):
+        step_ops(*inputs, ev=evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = 1e3 * wall / a.steps
+    names = ("slice_fwd", "deslice_fwd", "deslice_bwd", "slice_bwd")
+    per_op = {n: sum(e[i].elapsed_time(e[i + 1]) for e in evs) / a.steps
+              for i, n in enumerate(names)}
+    bytes_ = alg_bytes(B, N, H, D, DV)
+    flops = alg_flops(B, N, H, D, DV, G)
+    dom = max(per_op, key=per_op.get)
+    ach = bytes_[dom] / (per_op[dom] * 1e-3) / 1e9
+    total_bytes = sum(bytes_.values())
+    total_flops = sum(flops.values())
+    step_ach = total_bytes / (ms_step * 1e-3) / 1e9
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        v, n_s, thr = cpu_baseline(B, H, D, DV, G, layout)
+        cpu = {"value": round(v / 1e6, 4), "unit": "Mpoints/s", "cores": thr, "kind": "port",
+               "sample": "eager PyTorch softmax/einsum oracle (oracle/eager.py), fp32 fwd+bwd "
+                         "of the same coupling on %d of the %d points, median of 3 runs, "
+                         "torch threads=%d, os.cpu_count()=%d" % (n_s, N, thr, os.cpu_count())}
+
+    line = {
+        "metric": "slice+deslice fwd+bwd Mpoints/s at N=1M,H=8,D=32,G=32 (ms and peak HBM "
+                  "alongside)" if a.workload == "c2" else "slice+deslice fwd+bwd Mpoints/s",
+        "value": round(B * N / (ms_step * 1e-3) / 1e6, 3),
+        "unit": "Mpoints/s",
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": desc, "B": B, "N": N, "H": H, "D": D, "DV": DV, "G": G,
+                   "weight": layout, "dot": "ieee"},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "alg_bytes_per_launch": bytes_[dom], "ms_per_launch": round(per_op[dom], 4)},
+        "step_roofline": {"alg_bytes": total_bytes, "achieved_GBs": round(step_ach, 1),
+                          "hbm_frac": round(step_ach / HBM_PEAK_GBS, 4),
+                          "alg_flops": total_flops,
+                          "mfma_f32_frac": round(total_flops / (ms_step * 1e-3) / 1e12
+                                                 / MFMA_F32_TFLOPS, 4)},
+        "per_op_ms": {k: round(v, 4) for k, v in per_op.items()},
+        "peak_hbm_gb": round(peak_gb, 3),
+        "nxhxg_gb": round(B * N * H * G * 4 / 1e9, 3),
+        "deterministic": deterministic,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -220,13 +220,13 @@ int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_par
   hipStream_t st = (hipStream_t)stream;
   rc = hip_check(fs::launch_fused_slice_fwd(a, x->dtype, mode_of(p->dot, x->dtype), st), who);
   if (rc) return rc;
-  const int64_t wf = wave_floats(FS_OP_SLICE_FWD, p);
   const int G = a.G, DV = a.DV;
-  rc = hip_check(fs::launch_reduce_parts(a.part, wf, 0, G * DV, a.B, a.H, a.P, a.B, a.H, z_num, st),
-                 who);
-  if (rc) return rc;
+  fs::ReduceSegments rs{};
+  rs.seg[0] = {z_num, 0, G * DV, a.B, a.H, 1.f};
+  rs.seg[1] = {s, (int64_t)G * DV, G, a.B, a.H, 1.f};
+  rs.n = 2;
   return hip_check(
-      fs::launch_reduce_parts(a.part, wf, (int64_t)G * DV, G, a.B, a.H, a.P, a.B, a.H, s, st), who);
+      fs::launch_reduce(a.part, wave_floats(FS_OP_SLICE_FWD, p), a.B, a.H, a.P, rs, st), who);
 }
 
 int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float* tokens,
@@ -290,21 +290,15 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
   hipStream_t st = (hipStream_t)stream;
   rc = hip_check(fs::launch_fused_slice_bwd(a, x->dtype, mode_of(p->dot, x->dtype), st), who);
   if (rc) return rc;
-  const int64_t wf = wave_floats(FS_OP_SLICE_BWD, p);
   const int G = a.G, D = a.D;
-  rc = hip_check(fs::launch_reduce_parts(a.part, wf, 0, G * D, a.B, a.H, a.P,
-                                         Bo_of(p->w_stride_b, p->B), Ho_of(p->w_stride_h, p->H),
-                                         dweight, st),
-                 who);
-  if (!rc)
-    rc = hip_check(fs::launch_reduce_parts(a.part, wf, (int64_t)G * D, G, a.B, a.H, a.P,
-                                           Bo_of(p->b_stride_b, p->B),
-                                           Ho_of(p->b_stride_h, p->H), dbias, st),
-                   who);
-  if (!rc)
-    rc = hip_check(
-        fs::launch_reduce_scalar(a.part, wf, (int64_t)G * D + G, a.B, a.H, a.P, dtau, st), who);
-  return rc;
+  fs::ReduceSegments rs{};
+  rs.seg[0] = {dweight, 0, G * D, Bo_of(p->w_stride_b, p->B), Ho_of(p->w_stride_h, p->H), 1.f};
+  rs.seg[1] = {dbias, (int64_t)G * D, G, Bo_of(p->b_stride_b, p->B), Ho_of(p->b_stride_h, p->H),
+               1.f};
+  rs.seg[2] = {dtau, (int64_t)G * D + G, 1, 1, a.H, 1.f};
+  rs.n = 3;
+  return hip_check(
+      fs::launch_reduce(a.part, wave_floats(FS_OP_SLICE_BWD, p), a.B, a.H, a.P, rs, st), who);
 }
 
 int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float* tokens,
@@ -339,23 +333,16 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
   hipStream_t st = (hipStream_t)stream;
   rc = hip_check(fs::launch_fused_deslice_bwd(a, x->dtype, mode_of(p->dot, x->dtype), st), who);
   if (rc) return rc;
-  const int64_t wf = wave_floats(FS_OP_DESLICE_BWD, p);
   const int G = a.G, D = a.D, DV = a.DV;
   const int64_t offW = (int64_t)G * DV, offB = offW + (int64_t)G * D;
-  rc = hip_check(
-      fs::launch_reduce_parts(a.part, wf, 0, G * DV, a.B, a.H, a.P, a.B, a.H, dtokens, st), who);
-  if (!rc)
-    rc = hip_check(fs::launch_reduce_parts(a.part, wf, offW, G * D, a.B, a.H, a.P,
-                                           Bo_of(p->w_stride_b, p->B),
-                                           Ho_of(p->w_stride_h, p->H), dweight, st),
-                   who);
-  if (!rc)
-    rc = hip_check(fs::launch_reduce_parts(a.part, wf, offB, G, a.B, a.H, a.P,
-                                           Bo_of(p->b_stride_b, p->B),
-                                           Ho_of(p->b_stride_h, p->H), dbias, st),
-                   who);
-  if (!rc) rc = hip_check(fs::launch_reduce_scalar(a.part, wf, offB + G, a.B, a.H, a.P, dtau, st), who);
-  return rc;
+  fs::ReduceSegments rs{};
+  rs.seg[0] = {dtokens, 0, G * DV, a.B, a.H, 1.f};
+  rs.seg[1] = {dweight, offW, G * D, Bo_of(p->w_stride_b, p->B), Ho_of(p->w_stride_h, p->H), 1.f};
+  rs.seg[2] = {dbias, offB, G, Bo_of(p->b_stride_b, p->B), Ho_of(p->b_stride_h, p->H), 1.f};
+  rs.seg[3] = {dtau, offB + G, 1, 1, a.H, 1.f};
+  rs.n = 4;
+  return hip_check(
+      fs::launch_reduce(a.part, wave_floats(FS_OP_DESLICE_BWD, p), a.B, a.H, a.P, rs, st), who);
 }
 
 }  // extern "C"

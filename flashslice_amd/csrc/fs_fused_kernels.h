@@ -167,22 +167,36 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_fwd(Args a) {
   }
   const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
   const T* fb = (const T*)a.f + b * a.sfb + hd * a.sfh;
-  for (int t = blockIdx.x; t < a.ntiles; t += a.P) {
+  // the next tile's operands are loaded while the current one is computed
+  float xn[NDB][16], fn[NVB][16];
+  auto load_tile = [&](int t) {
     const int p0 = t * kTile, p = p0 + c;
-    const bool pv = p < N;
-    float xf[NDB][16];
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
-      load_frag_rows<T>(xf[db], xb + (int64_t)p * a.sxn, pv, 32 * db, D, a.vec_x, h);
+      load_frag_rows<T>(xn[db], xb + (int64_t)p * a.sxn, p < N, 32 * db, D, a.vec_x, h);
     // fx as [v-outer, point-inner]: a coalesced row read per register
-    float fT[NVB][16];
 #pragma unroll
     for (int vb = 0; vb < NVB; ++vb)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int pj = p0 + kmap(j, h), v = 32 * vb + c;
-        fT[vb][j] = (pj < N && v < DV) ? to_f<T>(fb[(int64_t)pj * a.sfn + v]) : 0.f;
+        fn[vb][j] = (pj < N && v < DV) ? to_f<T>(fb[(int64_t)pj * a.sfn + v]) : 0.f;
       }
+  };
+  if ((int)blockIdx.x < a.ntiles) load_tile(blockIdx.x);
+  for (int t = blockIdx.x; t < a.ntiles; t += a.P) {
+    const int p = t * kTile + c;
+    const bool pv = p < N;
+    float xf[NDB][16], fT[NVB][16];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) xf[db][j] = xn[db][j];
+#pragma unroll
+    for (int vb = 0; vb < NVB; ++vb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) fT[vb][j] = fn[vb][j];
+    if (t + a.P < a.ntiles) load_tile(t + a.P);
     float t2[NGB][16], w[NGB][16], m2, lsum;
     logits_tile<ML, NGB, NDB>(t2, wA, xf, bc, cst);
     softmax_tile<NGB>(w, m2, lsum, t2, pv);
@@ -234,13 +248,23 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_fwd(Args a) {
       load_frag_mat_colouter(tC[vb][gb], Tp, 32 * gb, G, 32 * vb, DV, c, h);
   const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
   T* ob = (T*)a.o1 + b * a.s1b + hd * a.s1h;
+  float xn[NDB][16];
+  auto load_tile = [&](int t) {
+    const int p = t * kTile + c;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+      load_frag_rows<T>(xn[db], xb + (int64_t)p * a.sxn, p < N, 32 * db, D, a.vec_x, h);
+  };
+  if ((int)blockIdx.x < a.ntiles) load_tile(blockIdx.x);
   for (int t = blockIdx.x; t < a.ntiles; t += a.P) {
     const int p = t * kTile + c;
     const bool pv = p < N;
     float xf[NDB][16];
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
-      load_frag_rows<T>(xf[db], xb + (int64_t)p * a.sxn, pv, 32 * db, D, a.vec_x, h);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) xf[db][j] = xn[db][j];
+    if (t + a.P < a.ntiles) load_tile(t + a.P);
     float t2[NGB][16], w[NGB][16], m2, lsum;
     logits_tile<ML, NGB, NDB>(t2, wA, xf, bc, cst);
     softmax_tile<NGB>(w, m2, lsum, t2, pv);
@@ -297,16 +321,30 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
   const T* fb = (const T*)a.f + b * a.sfb + hd * a.sfh;
   T* dxb = (T*)a.o1 + b * a.s1b + hd * a.s1h;
   T* dfb = (T*)a.o2 + b * a.s2b + hd * a.s2h;
+  float xn[NDB][16], fnx[NVB][16];
+  auto load_tile = [&](int t) {
+    const int p = t * kTile + c;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+      load_frag_rows<T>(xn[db], xb + (int64_t)p * a.sxn, p < N, 32 * db, D, a.vec_x, h);
+#pragma unroll
+    for (int vb = 0; vb < NVB; ++vb)
+      load_frag_rows<T>(fnx[vb], fb + (int64_t)p * a.sfn, p < N, 32 * vb, DV, a.vec_f, h);
+  };
+  if ((int)blockIdx.x < a.ntiles) load_tile(blockIdx.x);
   for (int t = blockIdx.x; t < a.ntiles; t += a.P) {
     const int p = t * kTile + c;
     const bool pv = p < N;
     float xf[NDB][16], ff[NVB][16];
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
-      load_frag_rows<T>(xf[db], xb + (int64_t)p * a.sxn, pv, 32 * db, D, a.vec_x, h);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) xf[db][j] = xn[db][j];
 #pragma unroll
     for (int vb = 0; vb < NVB; ++vb)
-      load_frag_rows<T>(ff[vb], fb + (int64_t)p * a.sfn, pv, 32 * vb, DV, a.vec_f, h);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) ff[vb][j] = fnx[vb][j];
+    if (t + a.P < a.ntiles) load_tile(t + a.P);
     float t2[NGB][16], w[NGB][16], m2, lsum;
     logits_tile<ML, NGB, NDB>(t2, wA, xf, bc, cst);
     softmax_tile<NGB>(w, m2, lsum, t2, pv);
@@ -406,16 +444,30 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_bwd(Args a) {
   const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
   const T* ob = (const T*)a.f + b * a.sfb + hd * a.sfh;
   T* dxb = (T*)a.o1 + b * a.s1b + hd * a.s1h;
+  float xn[NDB][16], fnx[NVB][16];
+  auto load_tile = [&](int t) {
+    const int p = t * kTile + c;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+      load_frag_rows<T>(xn[db], xb + (int64_t)p * a.sxn, p < N, 32 * db, D, a.vec_x, h);
+#pragma unroll
+    for (int vb = 0; vb < NVB; ++vb)
+      load_frag_rows<T>(fnx[vb], ob + (int64_t)p * a.sfn, p < N, 32 * vb, DV, a.vec_f, h);
+  };
+  if ((int)blockIdx.x < a.ntiles) load_tile(blockIdx.x);
   for (int t = blockIdx.x; t < a.ntiles; t += a.P) {
     const int p = t * kTile + c;
     const bool pv = p < N;
     float xf[NDB][16], of[NVB][16];
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
-      load_frag_rows<T>(xf[db], xb + (int64_t)p * a.sxn, pv, 32 * db, D, a.vec_x, h);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) xf[db][j] = xn[db][j];
 #pragma unroll
     for (int vb = 0; vb < NVB; ++vb)
-      load_frag_rows<T>(of[vb], ob + (int64_t)p * a.sfn, pv, 32 * vb, DV, a.vec_f, h);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) of[vb][j] = fnx[vb][j];
+    if (t + a.P < a.ntiles) load_tile(t + a.P);
     float t2[NGB][16], w[NGB][16], m2, lsum;
     logits_tile<ML, NGB, NDB>(t2, wA, xf, bc, cst);
     softmax_tile<NGB>(w, m2, lsum, t2, pv);

@@ -54,13 +54,21 @@ hipError_t launch_fused_slice_bwd(const Args& a, int dtype, int mode, hipStream_
 hipError_t launch_fused_deslice_bwd(const Args& a, int dtype, int mode, hipStream_t st);
 bool fused_fits(int D, int DV, int G);
 
-// deterministic reductions of per-wave partials
-// out[ob][oh][e] = scale * sum_{b -> ob} sum_{h -> oh} sum_{p < P} part[(b*H+h)*P + p][off + e]
-// where b maps to ob = (Bo > 1 ? b : 0) and h to oh = (Ho > 1 ? h : 0).
-hipError_t launch_reduce_parts(const float* part, int64_t wave_stride, int64_t off, int E, int B,
-                               int H, int P, int Bo, int Ho, float* out, hipStream_t st);
-// dtau[h] = sum_b sum_p part[(b*H+h)*P + p][off]
-hipError_t launch_reduce_scalar(const float* part, int64_t wave_stride, int64_t off, int B, int H,
-                                int P, float* out, hipStream_t st);
+// Deterministic reduction of per-wave partials (fs_reduce.hip). One output
+// segment: out[ob][oh][e] = scale * sum over the contributing waves
+// (b -> ob = Bo > 1 ? b : 0, h -> oh = Ho > 1 ? h : 0, every partition p)
+// of part[(b * H + h) * P + p][off + e], e < E.
+struct ReduceSegment {
+  float* out;
+  int64_t off;
+  int E, Bo, Ho;
+  float scale;
+};
+struct ReduceSegments {
+  ReduceSegment seg[4];
+  int n;
+};
+hipError_t launch_reduce(const float* part, int64_t wave_stride, int B, int H, int P,
+                         const ReduceSegments& segs, hipStream_t st);
 
 }  // namespace fs
