@@ -25,11 +25,13 @@ LIB_PATH = os.path.join(OUT_DIR, LIB_NAME)
 BUILD_DIR = os.path.join(os.path.dirname(HERE), "_build")
 
 ARCH = "gfx950"
-SOURCES = ("fs_fused.hip", "fs_reduce.hip", "fs_abi.cpp")
+SOURCES = ("fs_fused.hip", "fs_blocked.hip", "fs_reduce.hip", "fs_abi.cpp")
 # explicit instances of fused_launch<K, T, DK> (fs_fused_kernels.h), one
 # generated translation unit each so that they compile in parallel
 _FUSED_TYPES = (("float", (0,)), ("__bf16", (0, 1, 2)), ("_Float16", (0, 1, 2)))
 FUSED_INSTANCES = tuple((k, t, dk) for k in range(4) for t, dks in _FUSED_TYPES for dk in dks)
+# and of blocked_launch<K, T, DK> (fs_blocked_kernels.h)
+BLOCKED_INSTANCES = tuple((k, t, dk) for k in range(8) for t, dks in _FUSED_TYPES for dk in dks)
 FLAGS = [
     "--offload-arch=" + ARCH, "-O3", "-fPIC", "-std=c++17",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -49,11 +51,12 @@ def _generated_sources():
     gen = os.path.join(BUILD_DIR, "gen")
     os.makedirs(gen, exist_ok=True)
     out = []
-    for k, t, dk in FUSED_INSTANCES:
-        name = "fused_k%d_%s_dk%d.hip" % (k, t.strip("_"), dk)
-        text = ('#include "%s"\nnamespace fs {\ntemplate hipError_t fused_launch<%d, %s, %d>'
-                '(const Args&, hipStream_t);\n}\n' % (os.path.join(CSRC, "fs_fused_kernels.h"),
-                                                       k, t, dk))
+    units = [("fused", "fs_fused_kernels.h", "fused_launch", i) for i in FUSED_INSTANCES]
+    units += [("blocked", "fs_blocked_kernels.h", "blocked_launch", i) for i in BLOCKED_INSTANCES]
+    for fam, header, fn, (k, t, dk) in units:
+        name = "%s_k%d_%s_dk%d.hip" % (fam, k, t.strip("_"), dk)
+        text = ('#include "%s"\nnamespace fs {\ntemplate hipError_t %s<%d, %s, %d>'
+                '(const Args&, hipStream_t);\n}\n' % (os.path.join(CSRC, header), fn, k, t, dk))
         path = os.path.join(gen, name)
         if not os.path.exists(path) or open(path).read() != text:
             with open(path, "w") as f:

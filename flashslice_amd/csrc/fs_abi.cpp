@@ -1,10 +1,12 @@
 // C-ABI of the FlashSlice HIP kernels (declared in include/flashslice_hip.h).
 //
-// Validates every argument before any launch, picks the kernel family,
-// derives the launch geometry from the shape alone (never from the device,
-// so the per-wave partial layout -- and therefore every sum's order -- is
-// the same on every run and every GPU), launches the point-streaming
-// kernel and then the fixed-order reductions of its partials.
+// Validates every argument before any launch, picks the kernel family
+// (whole-G when the slot axis fits in registers, else G-blocked), derives the
+// launch geometry from the shape alone (never from the device, so the
+// per-wave partial layout -- and therefore every sum's order -- is the same
+// on every run and every GPU), carves the caller's workspace, launches the
+// point-streaming kernels and then the fixed-order reduction of their
+// partials. Nothing here allocates, frees or synchronises.
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -37,25 +39,34 @@ int32_t hip_check(hipError_t e, const char* what) {
   return fail(FS_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-// Blocks of the point-streaming grid: kTargetBlocks in total (two 4-wave
-// blocks per CU on a 256-CU MI355X), split over ceil(B*H / 4) block rows.
-constexpr int kTargetBlocks = 512;
-
+// ------------------------------------------------------------------ geometry
+// Point-owned grids: blocks of 4 waves on one (b, h), grid (P / 4, B * H);
+// the number of blocks targets the waves each kernel keeps resident per SIMD
+// on a 256-CU MI355X. Slot-owned grids add ceil(G / 32) along z.
 struct Geo {
   int ntiles, P;
 };
 
-Geo geometry(const fs_slice_params* p) {
+Geo geo_n(const fs_slice_params* p, int64_t target_blocks) {
   Geo g;
   g.ntiles = (int)((p->N + fs::kTile - 1) / fs::kTile);
-  const int64_t rows = (p->B * p->H + fs::kWavesPerBlock - 1) / fs::kWavesPerBlock;
-  int64_t P = (kTargetBlocks + rows - 1) / rows;
-  if (P > g.ntiles) P = g.ntiles;
-  if (P < 1) P = 1;
-  g.P = (int)P;
+  const int64_t bh = p->B * p->H;
+  int64_t bx = (target_blocks + bh - 1) / bh;
+  const int64_t need = (g.ntiles + fs::kWavesPerBlock - 1) / fs::kWavesPerBlock;
+  if (bx > need) bx = need;
+  if (bx < 1) bx = 1;
+  g.P = (int)(bx * fs::kWavesPerBlock);
   return g;
 }
 
+Geo geo_g(const fs_slice_params* p) {
+  const int64_t nsg = (p->G + 31) / 32;
+  return geo_n(p, (512 + nsg - 1) / nsg);
+}
+
+int64_t fused_target(int32_t op) { return op == FS_OP_DESLICE_FWD ? 1024 : 512; }
+
+// ------------------------------------------------------------------ checks
 int32_t check_params(const fs_slice_params* p, const char* who) {
   if (!p) return fail(FS_ERR_INVALID, "%s: params is NULL", who);
   if (p->B < 1 || p->N < 1 || p->H < 1)
@@ -65,12 +76,18 @@ int32_t check_params(const fs_slice_params* p, const char* who) {
     return fail(FS_ERR_INVALID, "%s: D and DV must be in [1, 256] (got %lld, %lld)", who,
                 (long long)p->D, (long long)p->DV);
   if (p->G < 1) return fail(FS_ERR_INVALID, "%s: G must be >= 1 (got %lld)", who, (long long)p->G);
+  if (p->G > (1 << 20))
+    return fail(FS_ERR_INVALID, "%s: G = %lld exceeds 2^20", who, (long long)p->G);
   if (p->N > (int64_t)0x7fffffff - 64)
     return fail(FS_ERR_INVALID, "%s: N = %lld exceeds 2^31 - 64", who, (long long)p->N);
+  if (p->B * p->H > 65535)
+    return fail(FS_ERR_INVALID, "%s: B * H = %lld exceeds 65535", who, (long long)(p->B * p->H));
   if (!p->weight || !p->bias || !p->tau)
     return fail(FS_ERR_INVALID, "%s: weight, bias and tau must be non-NULL", who);
   if (p->dot < 0 || p->dot > 4)
     return fail(FS_ERR_INVALID, "%s: dot level %d is not in [0, 4]", who, p->dot);
+  if (p->family < 0 || p->family > 2)
+    return fail(FS_ERR_INVALID, "%s: family %d is not 0, 1 or 2", who, p->family);
   return FS_OK;
 }
 
@@ -84,6 +101,9 @@ int32_t check_points(const fs_points* t, const char* name, int64_t width, const 
   return FS_OK;
 }
 
+// D and DV multiples of 32: every column group of a fragment is in range
+bool full_widths(const fs_slice_params* p) { return p->D % 32 == 0 && p->DV % 32 == 0; }
+
 int vec_ok(const fs_points* t) {
   const int64_t esz = t->dtype == fs::DT_F32 ? 4 : 2;
   const uintptr_t addr = (uintptr_t)t->data;
@@ -91,12 +111,19 @@ int vec_ok(const fs_points* t) {
          (t->stride_h % 4 == 0);
 }
 
-// the dot level as the fused kernels' DK: 0 all fp32, 1 bf16 value dots, 2 all bf16
+// the dot level as the kernels' DK: 0 all fp32, 1 bf16 value dots, 2 all bf16
 int mode_of(int dot, int dtype) {
   if (dtype == fs::DT_F32) return 0;
   if (dot == 2) return 1;
   if (dot == 3) return 2;
   return 0;
+}
+
+// 1 = whole-G, 2 = G-blocked; the whole-G family only when asked for
+// nothing else (family 0 or 1) and the shape fits
+int family_of(const fs_slice_params* p) {
+  if (p->family == 2) return 2;
+  return fs::fused_fits((int)p->D, (int)p->DV, (int)p->G) ? 1 : 2;
 }
 
 fs::Args base_args(const fs_slice_params* p, const Geo& g) {
@@ -117,6 +144,8 @@ fs::Args base_args(const fs_slice_params* p, const Geo& g) {
   a.G = (int)p->G;
   a.P = g.P;
   a.ntiles = g.ntiles;
+  a.nd = (int)((p->D + 31) / 32);
+  a.nv = (int)((p->DV + 31) / 32);
   return a;
 }
 
@@ -143,9 +172,44 @@ int64_t wave_floats(int32_t op, const fs_slice_params* p) {
   }
 }
 
-size_t fused_ws(int32_t op, const fs_slice_params* p) {
-  const Geo g = geometry(p);
-  return (size_t)(p->B * p->H * g.P * wave_floats(op, p)) * sizeof(float);
+// ------------------------------------------------------------------ workspace
+// The workspace of one op, carved in 256-byte aligned pieces.
+struct Workspace {
+  float* stats = nullptr;  // (B, H, 2, N) when the caller hands none in
+  float* delta = nullptr;  // (B, H, N)
+  float* lsum = nullptr;   // (B, H, N)
+  float* part2 = nullptr;  // (B H, P_n)
+  float* part = nullptr;   // (B H, P, wave_floats)
+  size_t bytes = 0;
+};
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+Workspace plan_ws(int32_t op, const fs_slice_params* p, char* base) {
+  Workspace w;
+  size_t off = 0;
+  auto take = [&](size_t nfloats) -> float* {
+    float* ptr = base ? (float*)(base + off) : nullptr;
+    off += align256(nfloats * sizeof(float));
+    return ptr;
+  };
+  const int64_t bh = p->B * p->H;
+  if (op == FS_OP_DESLICE_FWD || op == FS_OP_STATS) return w;
+  if (family_of(p) == 1) {
+    const Geo g = geo_n(p, fused_target(op));
+    w.part = take((size_t)(bh * g.P * wave_floats(op, p)));
+  } else {
+    const Geo gn = geo_n(p, 512), gg = geo_g(p);
+    w.stats = take((size_t)(bh * 2 * p->N));
+    if (op != FS_OP_SLICE_FWD) {
+      w.delta = take((size_t)(bh * p->N));
+      w.lsum = take((size_t)(bh * p->N));
+      w.part2 = take((size_t)(bh * gn.P));
+    }
+    w.part = take((size_t)(bh * gg.P * wave_floats(op, p)));
+  }
+  w.bytes = off;
+  return w;
 }
 
 int32_t check_ws(size_t need, size_t have, void* ws, const char* who) {
@@ -155,16 +219,36 @@ int32_t check_ws(size_t need, size_t have, void* ws, const char* who) {
   return FS_OK;
 }
 
-bool fused_family(const fs_slice_params* p) { return fs::fused_fits((int)p->D, (int)p->DV, (int)p->G); }
-
-int32_t unsupported_blocked(const char* who, const fs_slice_params* p) {
-  return fail(FS_ERR_UNSUPPORTED,
-              "%s: D=%lld DV=%lld G=%lld needs the G-blocked kernels, not in this build", who,
-              (long long)p->D, (long long)p->DV, (long long)p->G);
-}
-
 int Bo_of(int64_t stride_b, int64_t B) { return stride_b != 0 ? (int)B : 1; }
 int Ho_of(int64_t stride_h, int64_t H) { return stride_h != 0 ? (int)H : 1; }
+
+fs::ReduceSegment seg(const float* part, int64_t wstride, int64_t off, int P, int E, int Bo,
+                      int Ho, float* out) {
+  fs::ReduceSegment s;
+  s.part = part;
+  s.wstride = wstride;
+  s.off = off;
+  s.P = P;
+  s.E = E;
+  s.Bo = Bo;
+  s.Ho = Ho;
+  s.out = out;
+  return s;
+}
+
+// statistics of the logits into `stats` with the point-owned stats kernel
+int32_t run_stats(const fs_points* x, const fs_slice_params* p, float* stats, int two_pass,
+                  hipStream_t st, const char* who) {
+  const Geo g = geo_n(p, 512);
+  fs::Args a = base_args(p, g);
+  set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+  a.vec_x = vec_ok(x);
+  a.fast = a.vec_x && full_widths(p);
+  a.stats_out = stats;
+  a.two_pass = two_pass;
+  return hip_check(fs::launch_blocked(fs::BK_STATS, a, x->dtype, mode_of(p->dot, x->dtype), st),
+                   who);
+}
 
 }  // namespace
 
@@ -176,21 +260,23 @@ const char* fs_version(void) { return "flashslice_amd 0.1.0 (gfx950)"; }
 
 int32_t fs_family(const fs_slice_params* p) {
   if (!p) return 0;
-  return fused_family(p) ? 1 : 2;
+  return family_of(p);
 }
 
 size_t fs_workspace_bytes(int32_t op, const fs_slice_params* p) {
   if (check_params(p, "fs_workspace_bytes") != FS_OK) return 0;
-  if (op == FS_OP_DESLICE_FWD || op == FS_OP_STATS) return 0;
-  return fused_ws(op, p);
+  return plan_ws(op, p, nullptr).bytes;
 }
 
 int32_t fs_compute_stats(const fs_points* x, const fs_slice_params* p, float* stats,
                          int32_t two_pass, void* workspace, size_t workspace_bytes, void* stream) {
-  (void)x; (void)stats; (void)two_pass; (void)workspace; (void)workspace_bytes; (void)stream;
-  int32_t rc = check_params(p, "fs_compute_stats");
+  (void)workspace; (void)workspace_bytes;
+  const char* who = "fs_compute_stats";
+  int32_t rc = check_params(p, who);
+  if (!rc) rc = check_points(x, "x_mid", p->D, who);
   if (rc) return rc;
-  return unsupported_blocked("fs_compute_stats", p);
+  if (!stats) return fail(FS_ERR_INVALID, "%s: stats is NULL", who);
+  return run_stats(x, p, stats, two_pass ? 1 : 0, (hipStream_t)stream, who);
 }
 
 int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_params* p,
@@ -203,30 +289,52 @@ int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_par
   if (rc) return rc;
   if (fx->dtype != x->dtype) return fail(FS_ERR_INVALID, "%s: x_mid and fx_mid dtypes differ", who);
   if (!z_num || !s) return fail(FS_ERR_INVALID, "%s: z_num and s must be non-NULL", who);
-  // the whole-G kernels recompute the statistics exactly in their one pass,
-  // so handed-in statistics (of these very logits) are not needed there
-  (void)stats_in;
-  if (!fused_family(p)) return unsupported_blocked(who, p);
-  rc = check_ws(fused_ws(FS_OP_SLICE_FWD, p), workspace_bytes, workspace, who);
+  const Workspace ws = plan_ws(FS_OP_SLICE_FWD, p, (char*)workspace);
+  rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
   if (rc) return rc;
-  const Geo g = geometry(p);
-  fs::Args a = base_args(p, g);
-  set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
-  set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
-  a.vec_x = vec_ok(x);
-  a.vec_f = vec_ok(fx);
-  a.part = (float*)workspace;
-  a.stats_out = stats_out;
   hipStream_t st = (hipStream_t)stream;
-  rc = hip_check(fs::launch_fused_slice_fwd(a, x->dtype, mode_of(p->dot, x->dtype), st), who);
+  const int mode = mode_of(p->dot, x->dtype);
+  const int64_t wf = wave_floats(FS_OP_SLICE_FWD, p);
+  const int G = (int)p->G, DV = (int)p->DV;
+  Geo g;
+  if (family_of(p) == 1) {
+    // the whole-G kernels form the statistics exactly in their one pass, so
+    // handed-in statistics (of these very logits) are not needed
+    g = geo_n(p, fused_target(FS_OP_SLICE_FWD));
+    fs::Args a = base_args(p, g);
+    set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
+    a.vec_x = vec_ok(x);
+    a.vec_f = vec_ok(fx);
+    a.fast = a.vec_x && a.vec_f && full_widths(p);
+    a.part = ws.part;
+    a.stats_out = stats_out;
+    rc = hip_check(fs::launch_fused_slice_fwd(a, x->dtype, mode, st), who);
+  } else {
+    const float* stats = stats_in;
+    if (!stats) {
+      float* dst = stats_out ? stats_out : ws.stats;
+      rc = run_stats(x, p, dst, 0, st, who);
+      if (rc) return rc;
+      stats = dst;
+    }
+    g = geo_g(p);
+    fs::Args a = base_args(p, g);
+    set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
+    a.vec_x = vec_ok(x);
+    a.vec_f = vec_ok(fx);
+    a.fast = a.vec_x && a.vec_f && full_widths(p);
+    a.part = ws.part;
+    a.stats_in = stats;
+    rc = hip_check(fs::launch_blocked(fs::BK_SLICE_G, a, x->dtype, mode, st), who);
+  }
   if (rc) return rc;
-  const int G = a.G, DV = a.DV;
   fs::ReduceSegments rs{};
-  rs.seg[0] = {z_num, 0, G * DV, a.B, a.H, 1.f};
-  rs.seg[1] = {s, (int64_t)G * DV, G, a.B, a.H, 1.f};
+  rs.seg[0] = seg(ws.part, wf, 0, g.P, G * DV, (int)p->B, (int)p->H, z_num);
+  rs.seg[1] = seg(ws.part, wf, (int64_t)G * DV, g.P, G, (int)p->B, (int)p->H, s);
   rs.n = 2;
-  return hip_check(
-      fs::launch_reduce(a.part, wave_floats(FS_OP_SLICE_FWD, p), a.B, a.H, a.P, rs, st), who);
+  return hip_check(fs::launch_reduce((int)p->B, (int)p->H, rs, st), who);
 }
 
 int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float* tokens,
@@ -240,19 +348,34 @@ int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float
   if (rc) return rc;
   if (out->dtype != x->dtype) return fail(FS_ERR_INVALID, "%s: out and x_mid dtypes differ", who);
   if (!tokens) return fail(FS_ERR_INVALID, "%s: tokens is NULL", who);
-  (void)stats_in;
-  if (!fused_family(p)) return unsupported_blocked(who, p);
-  const Geo g = geometry(p);
+  hipStream_t st = (hipStream_t)stream;
+  const int mode = mode_of(p->dot, x->dtype);
+  if (family_of(p) == 1) {
+    const Geo g = geo_n(p, fused_target(FS_OP_DESLICE_FWD));
+    fs::Args a = base_args(p, g);
+    set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_out(out, &a.o1, &a.s1b, &a.s1n, &a.s1h);
+    a.vec_x = vec_ok(x);
+    a.vec_1 = vec_ok(out);
+    a.fast = a.vec_x && a.vec_1 && full_widths(p);
+    a.tok = tokens;
+    a.stats_out = stats_out;
+    return hip_check(fs::launch_fused_deslice_fwd(a, x->dtype, mode, st), who);
+  }
+  const Geo g = geo_n(p, 512);
   fs::Args a = base_args(p, g);
   set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
   set_out(out, &a.o1, &a.s1b, &a.s1n, &a.s1h);
-  a.stats_out = stats_out;
   a.vec_x = vec_ok(x);
   a.vec_1 = vec_ok(out);
+  a.fast = a.vec_x && a.vec_1 && full_widths(p);
   a.tok = tokens;
-  return hip_check(
-      fs::launch_fused_deslice_fwd(a, x->dtype, mode_of(p->dot, x->dtype), (hipStream_t)stream),
-      who);
+  if (stats_in) {
+    a.stats_in = stats_in;
+    return hip_check(fs::launch_blocked(fs::BK_DESLICE_N, a, x->dtype, mode, st), who);
+  }
+  a.stats_out = stats_out;  // may be NULL: then the statistics are not kept
+  return hip_check(fs::launch_blocked(fs::BK_DESLICE_ONLINE, a, x->dtype, mode, st), who);
 }
 
 int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_params* p,
@@ -270,35 +393,72 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     return fail(FS_ERR_INVALID, "%s: point tensors must share one dtype", who);
   if (!dz_num || !ds || !dweight || !dbias || !dtau)
     return fail(FS_ERR_INVALID, "%s: dz_num, ds, dweight, dbias, dtau must be non-NULL", who);
-  (void)stats_in;
-  if (!fused_family(p)) return unsupported_blocked(who, p);
-  rc = check_ws(fused_ws(FS_OP_SLICE_BWD, p), workspace_bytes, workspace, who);
+  const Workspace ws = plan_ws(FS_OP_SLICE_BWD, p, (char*)workspace);
+  rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
   if (rc) return rc;
-  const Geo g = geometry(p);
-  fs::Args a = base_args(p, g);
-  set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
-  set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
-  set_out(dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
-  set_out(dfx, &a.o2, &a.s2b, &a.s2n, &a.s2h);
-  a.vec_x = vec_ok(x);
-  a.vec_f = vec_ok(fx);
-  a.vec_1 = vec_ok(dx);
-  a.vec_2 = vec_ok(dfx);
-  a.tok = dz_num;
-  a.ds = ds;
-  a.part = (float*)workspace;
   hipStream_t st = (hipStream_t)stream;
-  rc = hip_check(fs::launch_fused_slice_bwd(a, x->dtype, mode_of(p->dot, x->dtype), st), who);
-  if (rc) return rc;
-  const int G = a.G, D = a.D;
+  const int mode = mode_of(p->dot, x->dtype);
+  const int64_t wf = wave_floats(FS_OP_SLICE_BWD, p);
+  const int G = (int)p->G, D = (int)p->D;
+  const int Bw = Bo_of(p->w_stride_b, p->B), Hw = Ho_of(p->w_stride_h, p->H);
+  const int Bb = Bo_of(p->b_stride_b, p->B), Hb = Ho_of(p->b_stride_h, p->H);
   fs::ReduceSegments rs{};
-  rs.seg[0] = {dweight, 0, G * D, Bo_of(p->w_stride_b, p->B), Ho_of(p->w_stride_h, p->H), 1.f};
-  rs.seg[1] = {dbias, (int64_t)G * D, G, Bo_of(p->b_stride_b, p->B), Ho_of(p->b_stride_h, p->H),
-               1.f};
-  rs.seg[2] = {dtau, (int64_t)G * D + G, 1, 1, a.H, 1.f};
+  if (family_of(p) == 1) {
+    const Geo g = geo_n(p, fused_target(FS_OP_SLICE_BWD));
+    fs::Args a = base_args(p, g);
+    set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
+    set_out(dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
+    set_out(dfx, &a.o2, &a.s2b, &a.s2n, &a.s2h);
+    a.vec_x = vec_ok(x);
+    a.vec_f = vec_ok(fx);
+    a.vec_1 = vec_ok(dx);
+    a.vec_2 = vec_ok(dfx);
+    a.fast = a.vec_x && a.vec_f && a.vec_1 && a.vec_2 && full_widths(p);
+    a.tok = dz_num;
+    a.ds = ds;
+    a.part = ws.part;
+    rc = hip_check(fs::launch_fused_slice_bwd(a, x->dtype, mode, st), who);
+    if (rc) return rc;
+    rs.seg[0] = seg(ws.part, wf, 0, g.P, G * D, Bw, Hw, dweight);
+    rs.seg[1] = seg(ws.part, wf, (int64_t)G * D, g.P, G, Bb, Hb, dbias);
+    rs.seg[2] = seg(ws.part, wf, (int64_t)G * D + G, g.P, 1, 1, (int)p->H, dtau);
+  } else {
+    const float* stats = stats_in;
+    if (!stats) {
+      rc = run_stats(x, p, ws.stats, 0, st, who);
+      if (rc) return rc;
+      stats = ws.stats;
+    }
+    const Geo gn = geo_n(p, 512), gg = geo_g(p);
+    fs::Args a = base_args(p, gn);
+    set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
+    set_out(dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
+    set_out(dfx, &a.o2, &a.s2b, &a.s2n, &a.s2h);
+    a.vec_x = vec_ok(x);
+    a.vec_f = vec_ok(fx);
+    a.vec_1 = vec_ok(dx);
+    a.vec_2 = vec_ok(dfx);
+    a.fast = a.vec_x && a.vec_f && a.vec_1 && a.vec_2 && full_widths(p);
+    a.tok = dz_num;
+    a.ds = ds;
+    a.stats_in = stats;
+    a.delta = ws.delta;
+    a.lsum = ws.lsum;
+    a.part2 = ws.part2;
+    rc = hip_check(fs::launch_blocked(fs::BK_SLICE_BWD_N, a, x->dtype, mode, st), who);
+    if (rc) return rc;
+    a.P = gg.P;
+    a.part = ws.part;
+    rc = hip_check(fs::launch_blocked(fs::BK_SLICE_BWD_G, a, x->dtype, mode, st), who);
+    if (rc) return rc;
+    rs.seg[0] = seg(ws.part, wf, 0, gg.P, G * D, Bw, Hw, dweight);
+    rs.seg[1] = seg(ws.part, wf, (int64_t)G * D, gg.P, G, Bb, Hb, dbias);
+    rs.seg[2] = seg(ws.part2, 1, 0, gn.P, 1, 1, (int)p->H, dtau);
+  }
   rs.n = 3;
-  return hip_check(
-      fs::launch_reduce(a.part, wave_floats(FS_OP_SLICE_BWD, p), a.B, a.H, a.P, rs, st), who);
+  return hip_check(fs::launch_reduce((int)p->B, (int)p->H, rs, st), who);
 }
 
 int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float* tokens,
@@ -316,33 +476,69 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
   if (!tokens || !dtokens || !dweight || !dbias || !dtau)
     return fail(FS_ERR_INVALID, "%s: tokens, dtokens, dweight, dbias, dtau must be non-NULL",
                 who);
-  (void)stats_in;
-  if (!fused_family(p)) return unsupported_blocked(who, p);
-  rc = check_ws(fused_ws(FS_OP_DESLICE_BWD, p), workspace_bytes, workspace, who);
+  const Workspace ws = plan_ws(FS_OP_DESLICE_BWD, p, (char*)workspace);
+  rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
   if (rc) return rc;
-  const Geo g = geometry(p);
-  fs::Args a = base_args(p, g);
-  set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
-  set_in(d_out, &a.f, &a.sfb, &a.sfn, &a.sfh);
-  set_out(dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
-  a.vec_x = vec_ok(x);
-  a.vec_f = vec_ok(d_out);
-  a.vec_1 = vec_ok(dx);
-  a.tok = tokens;
-  a.part = (float*)workspace;
   hipStream_t st = (hipStream_t)stream;
-  rc = hip_check(fs::launch_fused_deslice_bwd(a, x->dtype, mode_of(p->dot, x->dtype), st), who);
-  if (rc) return rc;
-  const int G = a.G, D = a.D, DV = a.DV;
+  const int mode = mode_of(p->dot, x->dtype);
+  const int64_t wf = wave_floats(FS_OP_DESLICE_BWD, p);
+  const int G = (int)p->G, D = (int)p->D, DV = (int)p->DV;
   const int64_t offW = (int64_t)G * DV, offB = offW + (int64_t)G * D;
+  const int Bw = Bo_of(p->w_stride_b, p->B), Hw = Ho_of(p->w_stride_h, p->H);
+  const int Bb = Bo_of(p->b_stride_b, p->B), Hb = Ho_of(p->b_stride_h, p->H);
   fs::ReduceSegments rs{};
-  rs.seg[0] = {dtokens, 0, G * DV, a.B, a.H, 1.f};
-  rs.seg[1] = {dweight, offW, G * D, Bo_of(p->w_stride_b, p->B), Ho_of(p->w_stride_h, p->H), 1.f};
-  rs.seg[2] = {dbias, offB, G, Bo_of(p->b_stride_b, p->B), Ho_of(p->b_stride_h, p->H), 1.f};
-  rs.seg[3] = {dtau, offB + G, 1, 1, a.H, 1.f};
+  if (family_of(p) == 1) {
+    const Geo g = geo_n(p, fused_target(FS_OP_DESLICE_BWD));
+    fs::Args a = base_args(p, g);
+    set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_in(d_out, &a.f, &a.sfb, &a.sfn, &a.sfh);
+    set_out(dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
+    a.vec_x = vec_ok(x);
+    a.vec_f = vec_ok(d_out);
+    a.vec_1 = vec_ok(dx);
+    a.fast = a.vec_x && a.vec_f && a.vec_1 && full_widths(p);
+    a.tok = tokens;
+    a.part = ws.part;
+    rc = hip_check(fs::launch_fused_deslice_bwd(a, x->dtype, mode, st), who);
+    if (rc) return rc;
+    rs.seg[0] = seg(ws.part, wf, 0, g.P, G * DV, (int)p->B, (int)p->H, dtokens);
+    rs.seg[1] = seg(ws.part, wf, offW, g.P, G * D, Bw, Hw, dweight);
+    rs.seg[2] = seg(ws.part, wf, offB, g.P, G, Bb, Hb, dbias);
+    rs.seg[3] = seg(ws.part, wf, offB + G, g.P, 1, 1, (int)p->H, dtau);
+  } else {
+    const float* stats = stats_in;
+    if (!stats) {
+      rc = run_stats(x, p, ws.stats, 0, st, who);
+      if (rc) return rc;
+      stats = ws.stats;
+    }
+    const Geo gn = geo_n(p, 512), gg = geo_g(p);
+    fs::Args a = base_args(p, gn);
+    set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_in(d_out, &a.f, &a.sfb, &a.sfn, &a.sfh);
+    set_out(dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
+    a.vec_x = vec_ok(x);
+    a.vec_f = vec_ok(d_out);
+    a.vec_1 = vec_ok(dx);
+    a.fast = a.vec_x && a.vec_f && a.vec_1 && full_widths(p);
+    a.tok = tokens;
+    a.stats_in = stats;
+    a.delta = ws.delta;
+    a.lsum = ws.lsum;
+    a.part2 = ws.part2;
+    rc = hip_check(fs::launch_blocked(fs::BK_DESLICE_BWD_N, a, x->dtype, mode, st), who);
+    if (rc) return rc;
+    a.P = gg.P;
+    a.part = ws.part;
+    rc = hip_check(fs::launch_blocked(fs::BK_DESLICE_BWD_G, a, x->dtype, mode, st), who);
+    if (rc) return rc;
+    rs.seg[0] = seg(ws.part, wf, 0, gg.P, G * DV, (int)p->B, (int)p->H, dtokens);
+    rs.seg[1] = seg(ws.part, wf, offW, gg.P, G * D, Bw, Hw, dweight);
+    rs.seg[2] = seg(ws.part, wf, offB, gg.P, G, Bb, Hb, dbias);
+    rs.seg[3] = seg(ws.part2, 1, 0, gn.P, 1, 1, (int)p->H, dtau);
+  }
   rs.n = 4;
-  return hip_check(
-      fs::launch_reduce(a.part, wave_floats(FS_OP_DESLICE_BWD, p), a.B, a.H, a.P, rs, st), who);
+  return hip_check(fs::launch_reduce((int)p->B, (int)p->H, rs, st), who);
 }
 
 }  // extern "C"

@@ -111,6 +111,23 @@ __device__ __forceinline__ void load_frag_rows(float (&f)[16], const T* row, boo
   }
 }
 
+// The branch-free form of load_frag_rows for full tiles of aligned rows
+// whose width is a multiple of 32: four vector loads of the (clamped,
+// always valid) row. Points beyond N read row N - 1; callers zero their
+// weights.
+template <typename T>
+__device__ __forceinline__ void load_frag_rows_fast(float (&f)[16], const T* row, int c0, int h) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    typename Vec4<T>::type v =
+        *reinterpret_cast<const typename Vec4<T>::type*>(row + c0 + 8 * q + 4 * h);
+    f[4 * q + 0] = to_f<T>(v[0]);
+    f[4 * q + 1] = to_f<T>(v[1]);
+    f[4 * q + 2] = to_f<T>(v[2]);
+    f[4 * q + 3] = to_f<T>(v[3]);
+  }
+}
+
 // Store a [point-outer, column-inner] fragment: row p (lane c), columns
 // c0 + kmap(r, h), masked to p < N and column < C.
 template <typename T>
@@ -158,6 +175,28 @@ __device__ __forceinline__ void load_frag_mat_colouter(float (&f)[16], const flo
     const int r = r0 + kmap(j, h);
     f[j] = (r < R && col < C) ? M[(int64_t)r * C + col] : 0.f;
   }
+}
+
+// Fragments of a matrix staged in LDS with row stride S (floats, S % 4 == 0
+// and S / 4 odd so that 8 consecutive rows fall in distinct bank groups):
+// [row-outer, col-inner] (four 16-byte reads) and [col-outer, row-inner]
+// (sixteen 4-byte reads), both bank-conflict-free.
+__device__ __forceinline__ void lds_frag_rowouter(float (&f)[16], const float* M, int S, int r0,
+                                                  int c0, int c, int h) {
+  const float* row = M + (r0 + c) * S + c0 + 4 * h;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 v = *reinterpret_cast<const float4*>(row + 8 * q);
+    f[4 * q + 0] = v.x;
+    f[4 * q + 1] = v.y;
+    f[4 * q + 2] = v.z;
+    f[4 * q + 3] = v.w;
+  }
+}
+__device__ __forceinline__ void lds_frag_colouter(float (&f)[16], const float* M, int S, int r0,
+                                                  int c0, int c, int h) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) f[j] = M[(r0 + kmap(j, h)) * S + c0 + c];
 }
 
 // [a-outer, b-inner] -> [b-outer, a-inner] through a wave-private LDS tile

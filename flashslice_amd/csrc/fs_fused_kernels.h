@@ -1,162 +1,87 @@
 // Whole-G ("fused") slice/deslice kernel templates for gfx950.
 //
-// One wave owns one (b, h) and a strided sequence of 32-point tiles
-// (tile t = pid, pid + P, ...; a static assignment, so per-wave partial sums
-// are deterministic). The whole slot axis G (padded to NGB blocks of 32) is
-// held in registers, so the softmax over G is exact in one pass and the
-// N x H x G weight tensor never exists outside registers. Every dot runs on
-// MFMA: v_mfma_f32_32x32x2_f32 for the ieee/tf32/tf32x3 levels and
-// v_mfma_f32_32x32x16_bf16 for the bf16 levels (see fs_device.h for the
-// fragment convention). Slot-indexed sums (z_num, s, dtokens, dW, db, dtau)
-// are accumulated per wave and written as per-wave partials that
-// fs_reduce.hip sums in a fixed order.
+// A block is four waves working on the same (b, h): the block stages that
+// head's slice projection W (G x D) and its tokens / dz_num (G x DV) in LDS
+// once, and each wave owns one point partition pid = 4 * blockIdx.x + wave,
+// i.e. the strided tile sequence t = pid, pid + P, ... (a static
+// assignment, so per-wave partial sums are deterministic). The whole slot
+// axis G (padded to NGB blocks of 32) is held in registers, so the softmax
+// over G is exact in one pass and the N x H x G weight tensor never exists
+// outside registers. Every dot runs on MFMA: v_mfma_f32_32x32x2_f32 for the
+// ieee/tf32/tf32x3 levels and v_mfma_f32_32x32x16_bf16 for the bf16 levels
+// (fragment convention: fs_device.h). Slot-indexed sums (z_num, s,
+// dtokens, dW, db, dtau) are accumulated per wave and written as per-wave
+// partials that fs_reduce.hip sums in a fixed order. The next tile's point
+// rows are loaded while the current tile is computed.
 //
 // Reference kernels these replace: _slice_fwd_kernel (slice_ops.py:554-599),
 // _deslice_fwd_kernel (:602-640), _slice_bwd_kernel (:643-710),
 // _deslice_bwd_kernel (:713-776).
 #pragma once
-#include "fs_device.h"
-#include "fs_internal.h"
+#include "fs_tile.h"
 
 namespace fs {
 
-// DK: 0 = every dot fp32 MFMA; 1 = value dots bf16 (reference level 2,
-// "bf16v"); 2 = every dot bf16 (level 3).
-template <int DK> struct Modes {
-  static constexpr int L = (DK == 2) ? MMA_BF16 : MMA_F32;
-  static constexpr int V = (DK >= 1) ? MMA_BF16 : MMA_F32;
+// LDS of one block: W [32 NGB][SW], tokens / dz_num [32 NGB][SV] (row
+// strides padded so fragment reads are conflict-free), one transpose tile
+// per wave.
+template <int NGB, int NDB, int NVB> struct Smem {
+  static constexpr int GP = 32 * NGB;
+  static constexpr int SW = 32 * NDB + 4, SV = 32 * NVB + 4;
+  static constexpr int W_OFF = 0, V_OFF = GP * SW, T_OFF = V_OFF + GP * SV;
+  static constexpr int TOTAL = T_OFF + kWavesPerBlock * kLdsTile;
 };
 
-// Per-wave constants of the logits: W as the A operand [g-outer, d-inner],
-// and bias * log2(e) / tau per output slot (-inf on padded slots).
-template <int NGB, int NDB>
-__device__ __forceinline__ void load_logit_consts(float (&wA)[NGB][NDB][16], float (&bc)[NGB][16],
-                                                  const float* Wp, const float* Bp, float cst,
-                                                  int G, int D, int c, int h) {
-#pragma unroll
-  for (int gb = 0; gb < NGB; ++gb) {
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-      load_frag_mat_rowouter(wA[gb][db], Wp, 32 * gb, G, 32 * db, D, c, h);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int g = 32 * gb + kmap(r, h);
-      bc[gb][r] = g < G ? Bp[g] * cst : -INFINITY;
-    }
+// Stage a small (G x C) fp32 matrix, zero-padded to (rows x cols), into LDS
+// with row stride S; all 256 threads of the block take part.
+__device__ __forceinline__ void stage_matrix(float* dst, int S, const float* src, int R, int C,
+                                             int rows, int cols) {
+  for (int i = threadIdx.x; i < rows * cols; i += 256) {
+    const int r = i / cols, col = i - r * cols;
+    dst[r * S + col] = (r < R && col < C) ? src[(int64_t)r * C + col] : 0.f;
   }
 }
 
-// Scaled logits t2 = (x . W + b) * log2(e) / tau of one tile, as
-// [point-outer, slot-inner] fragments.
-template <int ML, int NGB, int NDB>
-__device__ __forceinline__ void logits_tile(float (&t2)[NGB][16], const float (&wA)[NGB][NDB][16],
-                                            const float (&xf)[NDB][16], const float (&bc)[NGB][16],
-                                            float cst) {
-#pragma unroll
-  for (int gb = 0; gb < NGB; ++gb) {
-    f32x16 s = zero16();
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) s = mma32<ML>(wA[gb][db], xf[db], s);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) t2[gb][r] = fmaf(s[r], cst, bc[gb][r]);
+// Block prologue shared by the four kernels: head constants, LDS carve-up,
+// and the logits operands (W as the A operand [g-outer, d-inner] in
+// registers, bias * log2(e) / tau per output slot, -inf on padded slots).
+#define FS_PROLOGUE(NGB, NDB, NVB)                                                  \
+  using SM = Smem<NGB, NDB, NVB>;                                                   \
+  __shared__ float smem[SM::TOTAL];                                                 \
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;                       \
+  const int c = lane & 31, h = lane >> 5;                                           \
+  const int bh = blockIdx.y;                                                        \
+  const int b = bh / a.H, hd = bh - b * a.H;                                       \
+  const int pid = blockIdx.x * kWavesPerBlock + wid;                                \
+  const int G = a.G, D = a.D, DV = a.DV, N = a.N;                                   \
+  float* sW = smem + SM::W_OFF;                                                     \
+  float* sV = smem + SM::V_OFF;                                                     \
+  float* lds = smem + SM::T_OFF + wid * kLdsTile;                                   \
+  const float* Wp = a.W + b * a.swb + hd * a.swh;                                   \
+  const float* Bp = a.bias + b * a.sbb + hd * a.sbh;                                \
+  const float tauf = a.tau[hd];                                                     \
+  const float cst = (float)(1.4426950408889634 / (double)tauf);                    \
+  const float inv_tau = 1.f / tauf;                                                 \
+  const bool fast = a.fast != 0;                                                    \
+  (void)inv_tau; (void)sV; (void)lds; (void)DV;                                     \
+  stage_matrix(sW, SM::SW, Wp, G, D, SM::GP, 32 * NDB);                             \
+  if (a.tok) stage_matrix(sV, SM::SV, a.tok + (int64_t)bh * G * DV, G, DV, SM::GP, 32 * NVB); \
+  __syncthreads();                                                                  \
+  float wA[NGB][NDB][16], bc[NGB][16];                                              \
+  _Pragma("unroll") for (int gb = 0; gb < NGB; ++gb) {                              \
+    _Pragma("unroll") for (int db = 0; db < NDB; ++db)                              \
+      lds_frag_rowouter(wA[gb][db], sW, SM::SW, 32 * gb, 32 * db, c, h);            \
+    _Pragma("unroll") for (int r = 0; r < 16; ++r) {                                \
+      const int g = 32 * gb + kmap(r, h);                                           \
+      bc[gb][r] = g < G ? Bp[g] * cst : kNoSlot;                                  \
+    }                                                                               \
   }
-}
-
-// Softmax over the G slots of each point (lane pair c, c + 32 holds one
-// point). Returns w (zero for points beyond N) and the row max m2 (log2
-// units). The row sum is formed in a fixed order (lane-local, then the
-// partner), so both lanes of a pair hold the same value.
-template <int NGB>
-__device__ __forceinline__ void softmax_tile(float (&w)[NGB][16], float& m2, float& lsum,
-                                             const float (&t2)[NGB][16], bool pv) {
-  float m = -INFINITY;
-#pragma unroll
-  for (int gb = 0; gb < NGB; ++gb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) m = fmaxf(m, t2[gb][r]);
-  m = fmaxf(m, xor32(m));
-  float l = 0.f;
-#pragma unroll
-  for (int gb = 0; gb < NGB; ++gb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float e = __builtin_amdgcn_exp2f(t2[gb][r] - m);
-      w[gb][r] = e;
-      l += e;
-    }
-  l += xor32(l);
-  const float inv = 1.f / l;  // correctly rounded (no fast-math)
-#pragma unroll
-  for (int gb = 0; gb < NGB; ++gb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) w[gb][r] = pv ? w[gb][r] * inv : 0.f;
-  m2 = m;
-  lsum = l;
-}
-
-// Softmax statistics of one point in the reference layout (B, H, 2, N):
-// the row max of the natural-unit logits and the sum of exponentials
-// (reference blocked.py:1329-1335). Written by lane h = 0 of each pair.
-__device__ __forceinline__ void store_stats(float* stats, int bh, int N, int p, bool pv, int h,
-                                            float m2, float l) {
-  if (stats && pv && h == 0) {
-    float* base = stats + (int64_t)bh * 2 * N;
-    base[p] = m2 * kLn2;
-    base[N + p] = l;
-  }
-}
-
-// The softmax Jacobian of one tile given omega = dL/dw: Lb = w (omega -
-// delta), delta = sum_g w omega, both from the same rounded products.
-// Overwrites om with ab = Lb / tau and returns the row term
-// sum_g Lb (t2 - m2) of the temperature gradient (natural units up to a
-// factor ln 2; zero on lanes h = 1 and on points beyond N).
-template <int NGB>
-__device__ __forceinline__ float jacobian_tile(float (&om)[NGB][16], const float (&w)[NGB][16],
-                                               const float (&t2)[NGB][16], float m2,
-                                               float inv_tau, bool pv, int h) {
-  float d = 0.f;
-#pragma unroll
-  for (int gb = 0; gb < NGB; ++gb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) d += w[gb][r] * om[gb][r];
-  d += xor32(d);
-  float rt = 0.f;
-#pragma unroll
-  for (int gb = 0; gb < NGB; ++gb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float lb = w[gb][r] * (om[gb][r] - d);
-      rt += (w[gb][r] > 0.f) ? lb * (t2[gb][r] - m2) : 0.f;
-      om[gb][r] = lb * inv_tau;
-    }
-  rt += xor32(rt);
-  return (pv && h == 0) ? rt : 0.f;
-}
-
-#define FS_PROLOGUE                                                     \
-  __shared__ float smem[kWavesPerBlock * kLdsTile];                     \
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;           \
-  const int c = lane & 31, h = lane >> 5;                               \
-  const int bh = blockIdx.y * kWavesPerBlock + wid;                     \
-  if (bh >= a.B * a.H) return;                                          \
-  const int b = bh / a.H, hd = bh - b * a.H;                           \
-  float* lds = smem + wid * kLdsTile;                                   \
-  const float* Wp = a.W + b * a.swb + hd * a.swh;                       \
-  const float* Bp = a.bias + b * a.sbb + hd * a.sbh;                    \
-  const float tauf = a.tau[hd];                                         \
-  const float cst = (float)(1.4426950408889634 / (double)tauf);        \
-  const float inv_tau = 1.f / tauf;                                     \
-  (void)inv_tau; (void)lds;
 
 // ------------------------------------------------------------------ slice fwd
 template <typename T, int DK, int NGB, int NDB, int NVB>
 __global__ __launch_bounds__(256, 2) void k_fused_slice_fwd(Args a) {
   constexpr int ML = Modes<DK>::L, MV = Modes<DK>::V;
-  FS_PROLOGUE
-  const int G = a.G, D = a.D, DV = a.DV, N = a.N;
-  float wA[NGB][NDB][16], bc[NGB][16];
-  load_logit_consts<NGB, NDB>(wA, bc, Wp, Bp, cst, G, D, c, h);
+  FS_PROLOGUE(NGB, NDB, NVB)
   f32x16 zacc[NGB][NVB];
   float sacc[NGB];
 #pragma unroll
@@ -170,32 +95,27 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_fwd(Args a) {
   // the next tile's operands are loaded while the current one is computed
   float xn[NDB][16], fn[NVB][16];
   auto load_tile = [&](int t) {
-    const int p0 = t * kTile, p = p0 + c;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-      load_frag_rows<T>(xn[db], xb + (int64_t)p * a.sxn, p < N, 32 * db, D, a.vec_x, h);
-    // fx as [v-outer, point-inner]: a coalesced row read per register
+    const int p0 = t * kTile;
+    load_rows<T, NDB>(xn, xb, a.sxn, p0 + c, N, D, fast, a.vec_x, h);
+    // fx as [v-outer, point-inner]: one coalesced row read per register
 #pragma unroll
     for (int vb = 0; vb < NVB; ++vb)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int pj = p0 + kmap(j, h), v = 32 * vb + c;
-        fn[vb][j] = (pj < N && v < DV) ? to_f<T>(fb[(int64_t)pj * a.sfn + v]) : 0.f;
+        if (fast)
+          fn[vb][j] = to_f<T>(fb[(int64_t)(pj < N ? pj : N - 1) * a.sfn + v]);
+        else
+          fn[vb][j] = (pj < N && v < DV) ? to_f<T>(fb[(int64_t)pj * a.sfn + v]) : 0.f;
       }
   };
-  if ((int)blockIdx.x < a.ntiles) load_tile(blockIdx.x);
-  for (int t = blockIdx.x; t < a.ntiles; t += a.P) {
+  if (pid < a.ntiles) load_tile(pid);
+  for (int t = pid; t < a.ntiles; t += a.P) {
     const int p = t * kTile + c;
     const bool pv = p < N;
     float xf[NDB][16], fT[NVB][16];
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) xf[db][j] = xn[db][j];
-#pragma unroll
-    for (int vb = 0; vb < NVB; ++vb)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) fT[vb][j] = fn[vb][j];
+    copy_frags<T, NDB>(xf, xn);
+    copy_frags<T, NVB>(fT, fn);
     if (t + a.P < a.ntiles) load_tile(t + a.P);
     float t2[NGB][16], w[NGB][16], m2, lsum;
     logits_tile<ML, NGB, NDB>(t2, wA, xf, bc, cst);
@@ -213,7 +133,7 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_fwd(Args a) {
       sacc[gb] += s;
     }
   }
-  float* pw = a.part + ((int64_t)bh * a.P + blockIdx.x) * part_floats_slice_fwd(G, DV);
+  float* pw = a.part + ((int64_t)bh * a.P + pid) * part_floats_slice_fwd(G, DV);
 #pragma unroll
   for (int gb = 0; gb < NGB; ++gb) {
     const int g = 32 * gb + c;
@@ -235,46 +155,35 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_fwd(Args a) {
 template <typename T, int DK, int NGB, int NDB, int NVB>
 __global__ __launch_bounds__(256, 2) void k_fused_deslice_fwd(Args a) {
   constexpr int ML = Modes<DK>::L, MV = Modes<DK>::V;
-  FS_PROLOGUE
-  const int G = a.G, D = a.D, DV = a.DV, N = a.N;
-  float wA[NGB][NDB][16], bc[NGB][16];
-  load_logit_consts<NGB, NDB>(wA, bc, Wp, Bp, cst, G, D, c, h);
-  const float* Tp = a.tok + (int64_t)bh * G * DV;
+  FS_PROLOGUE(NGB, NDB, NVB)
   float tC[NVB][NGB][16];  // tokens as [v-outer, g-inner]
 #pragma unroll
   for (int vb = 0; vb < NVB; ++vb)
 #pragma unroll
     for (int gb = 0; gb < NGB; ++gb)
-      load_frag_mat_colouter(tC[vb][gb], Tp, 32 * gb, G, 32 * vb, DV, c, h);
+      lds_frag_colouter(tC[vb][gb], sV, SM::SV, 32 * gb, 32 * vb, c, h);
   const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
   T* ob = (T*)a.o1 + b * a.s1b + hd * a.s1h;
   float xn[NDB][16];
-  auto load_tile = [&](int t) {
-    const int p = t * kTile + c;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-      load_frag_rows<T>(xn[db], xb + (int64_t)p * a.sxn, p < N, 32 * db, D, a.vec_x, h);
-  };
-  if ((int)blockIdx.x < a.ntiles) load_tile(blockIdx.x);
-  for (int t = blockIdx.x; t < a.ntiles; t += a.P) {
+  if (pid < a.ntiles) load_rows<T, NDB>(xn, xb, a.sxn, pid * kTile + c, N, D, fast, a.vec_x, h);
+  for (int t = pid; t < a.ntiles; t += a.P) {
     const int p = t * kTile + c;
     const bool pv = p < N;
     float xf[NDB][16];
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) xf[db][j] = xn[db][j];
-    if (t + a.P < a.ntiles) load_tile(t + a.P);
+    copy_frags<T, NDB>(xf, xn);
+    if (t + a.P < a.ntiles)
+      load_rows<T, NDB>(xn, xb, a.sxn, (t + a.P) * kTile + c, N, D, fast, a.vec_x, h);
     float t2[NGB][16], w[NGB][16], m2, lsum;
     logits_tile<ML, NGB, NDB>(t2, wA, xf, bc, cst);
     softmax_tile<NGB>(w, m2, lsum, t2, pv);
     store_stats(a.stats_out, bh, N, p, pv, h, m2, lsum);
+    T* orow = ob + (int64_t)p * a.s1n;
 #pragma unroll
     for (int vb = 0; vb < NVB; ++vb) {
       f32x16 o = zero16();
 #pragma unroll
       for (int gb = 0; gb < NGB; ++gb) o = mma32<MV>(tC[vb][gb], w[gb], o);
-      store_frag_rows<T>(ob + (int64_t)p * a.s1n, o, pv, 32 * vb, DV, a.vec_1, h);
+      store_rows<T>(orow, o, pv, 32 * vb, DV, fast, a.vec_1, h);
     }
   }
 }
@@ -283,32 +192,18 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_fwd(Args a) {
 template <typename T, int DK, int NGB, int NDB, int NVB>
 __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
   constexpr int ML = Modes<DK>::L, MV = Modes<DK>::V;
-  FS_PROLOGUE
-  const int G = a.G, D = a.D, DV = a.DV, N = a.N;
-  float wA[NGB][NDB][16], bc[NGB][16];
-  load_logit_consts<NGB, NDB>(wA, bc, Wp, Bp, cst, G, D, c, h);
-  const float* Zp = a.tok + (int64_t)bh * G * DV;
+  FS_PROLOGUE(NGB, NDB, NVB)
+  // sW holds W, sV holds dz_num; dz_num is read per tile as [g-outer,
+  // v-inner] (omega) and [v-outer, g-inner] (dfx), W as [d-outer, g-inner].
   const float* Sp = a.ds + (int64_t)bh * G;
-  float wC[NDB][NGB][16];   // W as [d-outer, g-inner]
-  float zR[NGB][NVB][16];   // dz_num as [g-outer, v-inner]
-  float zC[NVB][NGB][16];   // dz_num as [v-outer, g-inner]
-  float dsv[NGB][16];       // d s per output slot
+  float dsv[NGB][16];  // d s per output slot
 #pragma unroll
-  for (int gb = 0; gb < NGB; ++gb) {
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-      load_frag_mat_colouter(wC[db][gb], Wp, 32 * gb, G, 32 * db, D, c, h);
-#pragma unroll
-    for (int vb = 0; vb < NVB; ++vb) {
-      load_frag_mat_rowouter(zR[gb][vb], Zp, 32 * gb, G, 32 * vb, DV, c, h);
-      load_frag_mat_colouter(zC[vb][gb], Zp, 32 * gb, G, 32 * vb, DV, c, h);
-    }
+  for (int gb = 0; gb < NGB; ++gb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int g = 32 * gb + kmap(r, h);
       dsv[gb][r] = g < G ? Sp[g] : 0.f;
     }
-  }
   f32x16 dW[NGB][NDB];
   float dbacc[NGB], dtacc = 0.f;
 #pragma unroll
@@ -324,26 +219,16 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
   float xn[NDB][16], fnx[NVB][16];
   auto load_tile = [&](int t) {
     const int p = t * kTile + c;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-      load_frag_rows<T>(xn[db], xb + (int64_t)p * a.sxn, p < N, 32 * db, D, a.vec_x, h);
-#pragma unroll
-    for (int vb = 0; vb < NVB; ++vb)
-      load_frag_rows<T>(fnx[vb], fb + (int64_t)p * a.sfn, p < N, 32 * vb, DV, a.vec_f, h);
+    load_rows<T, NDB>(xn, xb, a.sxn, p, N, D, fast, a.vec_x, h);
+    load_rows<T, NVB>(fnx, fb, a.sfn, p, N, DV, fast, a.vec_f, h);
   };
-  if ((int)blockIdx.x < a.ntiles) load_tile(blockIdx.x);
-  for (int t = blockIdx.x; t < a.ntiles; t += a.P) {
+  if (pid < a.ntiles) load_tile(pid);
+  for (int t = pid; t < a.ntiles; t += a.P) {
     const int p = t * kTile + c;
     const bool pv = p < N;
     float xf[NDB][16], ff[NVB][16];
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) xf[db][j] = xn[db][j];
-#pragma unroll
-    for (int vb = 0; vb < NVB; ++vb)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) ff[vb][j] = fnx[vb][j];
+    copy_frags<T, NDB>(xf, xn);
+    copy_frags<T, NVB>(ff, fnx);
     if (t + a.P < a.ntiles) load_tile(t + a.P);
     float t2[NGB][16], w[NGB][16], m2, lsum;
     logits_tile<ML, NGB, NDB>(t2, wA, xf, bc, cst);
@@ -353,8 +238,12 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
     for (int vb = 0; vb < NVB; ++vb) {
       f32x16 o = zero16();
 #pragma unroll
-      for (int gb = 0; gb < NGB; ++gb) o = mma32<MV>(zC[vb][gb], w[gb], o);
-      store_frag_rows<T>(dfb + (int64_t)p * a.s2n, o, pv, 32 * vb, DV, a.vec_2, h);
+      for (int gb = 0; gb < NGB; ++gb) {
+        float zc[16];
+        lds_frag_colouter(zc, sV, SM::SV, 32 * gb, 32 * vb, c, h);
+        o = mma32<MV>(zc, w[gb], o);
+      }
+      store_rows<T>(dfb + (int64_t)p * a.s2n, o, pv, 32 * vb, DV, fast, a.vec_2, h);
     }
     // omega = fx . dz_num + ds
     float om[NGB][16];
@@ -362,7 +251,11 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
     for (int gb = 0; gb < NGB; ++gb) {
       f32x16 o = zero16();
 #pragma unroll
-      for (int vb = 0; vb < NVB; ++vb) o = mma32<MV>(zR[gb][vb], ff[vb], o);
+      for (int vb = 0; vb < NVB; ++vb) {
+        float zr[16];
+        lds_frag_rowouter(zr, sV, SM::SV, 32 * gb, 32 * vb, c, h);
+        o = mma32<MV>(zr, ff[vb], o);
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) om[gb][r] = o[r] + dsv[gb][r];
     }
@@ -372,8 +265,12 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
     for (int db = 0; db < NDB; ++db) {
       f32x16 o = zero16();
 #pragma unroll
-      for (int gb = 0; gb < NGB; ++gb) o = mma32<MV>(wC[db][gb], om[gb], o);
-      store_frag_rows<T>(dxb + (int64_t)p * a.s1n, o, pv, 32 * db, D, a.vec_1, h);
+      for (int gb = 0; gb < NGB; ++gb) {
+        float wc[16];
+        lds_frag_colouter(wc, sW, SM::SW, 32 * gb, 32 * db, c, h);
+        o = mma32<MV>(wc, om[gb], o);
+      }
+      store_rows<T>(dxb + (int64_t)p * a.s1n, o, pv, 32 * db, D, fast, a.vec_1, h);
     }
     // dW += ab^T x, db += sum_n ab
     float xT[NDB][16];
@@ -391,7 +288,7 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
       dbacc[gb] += s;
     }
   }
-  float* pw = a.part + ((int64_t)bh * a.P + blockIdx.x) * part_floats_slice_bwd(G, D);
+  float* pw = a.part + ((int64_t)bh * a.P + pid) * part_floats_slice_bwd(G, D);
 #pragma unroll
   for (int gb = 0; gb < NGB; ++gb) {
     const int g = 32 * gb + c;
@@ -415,22 +312,9 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
 template <typename T, int DK, int NGB, int NDB, int NVB>
 __global__ __launch_bounds__(256, 2) void k_fused_deslice_bwd(Args a) {
   constexpr int ML = Modes<DK>::L, MV = Modes<DK>::V;
-  FS_PROLOGUE
-  const int G = a.G, D = a.D, DV = a.DV, N = a.N;
-  float wA[NGB][NDB][16], bc[NGB][16];
-  load_logit_consts<NGB, NDB>(wA, bc, Wp, Bp, cst, G, D, c, h);
-  const float* Tp = a.tok + (int64_t)bh * G * DV;
-  float wC[NDB][NGB][16];   // W as [d-outer, g-inner]
-  float tR[NGB][NVB][16];   // tokens as [g-outer, v-inner]
-#pragma unroll
-  for (int gb = 0; gb < NGB; ++gb) {
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-      load_frag_mat_colouter(wC[db][gb], Wp, 32 * gb, G, 32 * db, D, c, h);
-#pragma unroll
-    for (int vb = 0; vb < NVB; ++vb)
-      load_frag_mat_rowouter(tR[gb][vb], Tp, 32 * gb, G, 32 * vb, DV, c, h);
-  }
+  FS_PROLOGUE(NGB, NDB, NVB)
+  // sW holds W (read as [d-outer, g-inner] for dx), sV the tokens (read as
+  // [g-outer, v-inner] for omega).
   f32x16 dT[NGB][NVB], dW[NGB][NDB];
   float dbacc[NGB], dtacc = 0.f;
 #pragma unroll
@@ -447,31 +331,21 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_bwd(Args a) {
   float xn[NDB][16], fnx[NVB][16];
   auto load_tile = [&](int t) {
     const int p = t * kTile + c;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-      load_frag_rows<T>(xn[db], xb + (int64_t)p * a.sxn, p < N, 32 * db, D, a.vec_x, h);
-#pragma unroll
-    for (int vb = 0; vb < NVB; ++vb)
-      load_frag_rows<T>(fnx[vb], ob + (int64_t)p * a.sfn, p < N, 32 * vb, DV, a.vec_f, h);
+    load_rows<T, NDB>(xn, xb, a.sxn, p, N, D, fast, a.vec_x, h);
+    load_rows<T, NVB>(fnx, ob, a.sfn, p, N, DV, fast, a.vec_f, h);
   };
-  if ((int)blockIdx.x < a.ntiles) load_tile(blockIdx.x);
-  for (int t = blockIdx.x; t < a.ntiles; t += a.P) {
+  if (pid < a.ntiles) load_tile(pid);
+  for (int t = pid; t < a.ntiles; t += a.P) {
     const int p = t * kTile + c;
     const bool pv = p < N;
     float xf[NDB][16], of[NVB][16];
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) xf[db][j] = xn[db][j];
-#pragma unroll
-    for (int vb = 0; vb < NVB; ++vb)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) of[vb][j] = fnx[vb][j];
+    copy_frags<T, NDB>(xf, xn);
+    copy_frags<T, NVB>(of, fnx);
     if (t + a.P < a.ntiles) load_tile(t + a.P);
     float t2[NGB][16], w[NGB][16], m2, lsum;
     logits_tile<ML, NGB, NDB>(t2, wA, xf, bc, cst);
     softmax_tile<NGB>(w, m2, lsum, t2, pv);
-    // dtokens += w^T d_out
+    // dtokens += w^T d_out (rows of d_out beyond N meet zero weights)
     float oT[NVB][16];
 #pragma unroll
     for (int vb = 0; vb < NVB; ++vb) transpose32(oT[vb], of[vb], lds, c, h);
@@ -488,7 +362,11 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_bwd(Args a) {
     for (int gb = 0; gb < NGB; ++gb) {
       f32x16 o = zero16();
 #pragma unroll
-      for (int vb = 0; vb < NVB; ++vb) o = mma32<MV>(tR[gb][vb], of[vb], o);
+      for (int vb = 0; vb < NVB; ++vb) {
+        float tr[16];
+        lds_frag_rowouter(tr, sV, SM::SV, 32 * gb, 32 * vb, c, h);
+        o = mma32<MV>(tr, of[vb], o);
+      }
       from16(om[gb], o);
     }
     dtacc += jacobian_tile<NGB>(om, w, t2, m2, inv_tau, pv, h);
@@ -496,8 +374,12 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_bwd(Args a) {
     for (int db = 0; db < NDB; ++db) {
       f32x16 o = zero16();
 #pragma unroll
-      for (int gb = 0; gb < NGB; ++gb) o = mma32<MV>(wC[db][gb], om[gb], o);
-      store_frag_rows<T>(dxb + (int64_t)p * a.s1n, o, pv, 32 * db, D, a.vec_1, h);
+      for (int gb = 0; gb < NGB; ++gb) {
+        float wc[16];
+        lds_frag_colouter(wc, sW, SM::SW, 32 * gb, 32 * db, c, h);
+        o = mma32<MV>(wc, om[gb], o);
+      }
+      store_rows<T>(dxb + (int64_t)p * a.s1n, o, pv, 32 * db, D, fast, a.vec_1, h);
     }
     float xT[NDB][16];
 #pragma unroll
@@ -514,7 +396,7 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_bwd(Args a) {
       dbacc[gb] += s;
     }
   }
-  float* pw = a.part + ((int64_t)bh * a.P + blockIdx.x) * part_floats_deslice_bwd(G, D, DV);
+  float* pw = a.part + ((int64_t)bh * a.P + pid) * part_floats_deslice_bwd(G, D, DV);
   const int64_t offW = (int64_t)G * DV, offB = offW + (int64_t)G * D;
 #pragma unroll
   for (int gb = 0; gb < NGB; ++gb) {
@@ -559,11 +441,11 @@ __host__ inline int blocks_of(int n) {
 
 // Launch the fused kernel of kind K for point dtype T and dot kind DK.
 // Explicitly instantiated in the generated translation units (build.py),
-// one per (K, T, DK), so they compile in parallel.
+// one per (K, T, DK), so they compile in parallel. Grid: (P / 4, B * H).
 template <int K, typename T, int DK>
 hipError_t fused_launch(const Args& a, hipStream_t st) {
   const int g = blocks_of(a.G), d = blocks_of(a.D), v = blocks_of(a.DV);
-  const dim3 grid(a.P, (a.B * a.H + kWavesPerBlock - 1) / kWavesPerBlock), block(256);
+  const dim3 grid(a.P / kWavesPerBlock, a.B * a.H), block(256);
 #define FS_TRY(G_, D_, V_)                                                                    \
   if (g == G_ && d == D_ && v == V_) {                                                        \
     if constexpr (K == FK_SLICE_FWD)                                                          \

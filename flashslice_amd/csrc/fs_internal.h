@@ -25,13 +25,17 @@ struct Args {
   const float* ds;                         // (B, H, G): d s (slice bwd)
   const float* stats_in;                   // (B, H, 2, N) or null
   float* stats_out;                        // (B, H, 2, N) or null
-  float* delta;                            // (B, H, N) scratch (blocked bwd)
+  float* delta;                            // (B, H, N) softmax-Jacobian row terms (blocked bwd)
+  float* lsum;                             // (B, H, N) row sums formed by the point-owned bwd pass
   float* part;                             // per-wave partials (workspace)
+  float* part2;                            // per-wave dtau partials of point-owned kernels
   int B, N, H, D, DV, G;
-  int P;                                   // point partitions per (b, h)
+  int P;                                   // point partitions per (b, h), a multiple of 4
   int ntiles;                              // ceil(N / 32)
   int vec_x, vec_f, vec_1, vec_2;          // 4-element alignment of rows
-  int nblk;                                // slot blocks held per wave (blocked family)
+  int fast;                                // all rows aligned, D and DV multiples of 32
+  int nd, nv;                              // 32-wide blocks of D and DV (blocked family)
+  int two_pass;                            // statistics: max pass, then sum pass
 };
 
 // Partial-buffer layout of one wave (floats), fused family:
@@ -54,21 +58,37 @@ hipError_t launch_fused_slice_bwd(const Args& a, int dtype, int mode, hipStream_
 hipError_t launch_fused_deslice_bwd(const Args& a, int dtype, int mode, hipStream_t st);
 bool fused_fits(int D, int DV, int G);
 
+// G-blocked family (any G; fs_blocked.hip). Point-owned kernels ("_n") run
+// on grid (P / 4, B * H); slot-owned kernels ("_g") on (P / 4, B * H,
+// ceil(G / 32)) and write the same per-wave partial layout as the fused
+// family (every wave its own 32 slot rows).
+enum BlockedKind {
+  BK_STATS = 0,          // (m, l) per point, online or two-pass
+  BK_DESLICE_N = 1,      // out from saved statistics
+  BK_DESLICE_ONLINE = 2, // out and the statistics in one online pass
+  BK_SLICE_G = 3,        // z_num, s partials from saved statistics
+  BK_SLICE_BWD_N = 4,    // dfx, delta, dx, dtau partials
+  BK_SLICE_BWD_G = 5,    // dW, db partials
+  BK_DESLICE_BWD_N = 6,  // delta, dx, dtau partials
+  BK_DESLICE_BWD_G = 7   // dtokens, dW, db partials
+};
+hipError_t launch_blocked(int kind, const Args& a, int dtype, int mode, hipStream_t st);
+int blocked_width_blocks(int D, int DV);  // 1, 2, 4 or 8 (0 if D or DV > 256)
+
 // Deterministic reduction of per-wave partials (fs_reduce.hip). One output
-// segment: out[ob][oh][e] = scale * sum over the contributing waves
-// (b -> ob = Bo > 1 ? b : 0, h -> oh = Ho > 1 ? h : 0, every partition p)
-// of part[(b * H + h) * P + p][off + e], e < E.
+// segment: out[ob][oh][e] = sum over the contributing waves (b -> ob =
+// Bo > 1 ? b : 0, h -> oh = Ho > 1 ? h : 0, every partition p < P) of
+// part[((b * H + h) * P + p) * wstride + off + e], e < E.
 struct ReduceSegment {
+  const float* part;
+  int64_t wstride, off;
+  int P, E, Bo, Ho;
   float* out;
-  int64_t off;
-  int E, Bo, Ho;
-  float scale;
 };
 struct ReduceSegments {
   ReduceSegment seg[4];
   int n;
 };
-hipError_t launch_reduce(const float* part, int64_t wave_stride, int B, int H, int P,
-                         const ReduceSegments& segs, hipStream_t st);
+hipError_t launch_reduce(int B, int H, const ReduceSegments& segs, hipStream_t st);
 
 }  // namespace fs

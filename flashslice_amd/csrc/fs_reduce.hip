@@ -16,9 +16,7 @@
 
 namespace fs {
 
-__global__ __launch_bounds__(256) void k_reduce_segments(const float* __restrict__ part,
-                                                         int64_t wstride, int B, int H, int P,
-                                                         ReduceSegments segs) {
+__global__ __launch_bounds__(256) void k_reduce_segments(int B, int H, ReduceSegments segs) {
   __shared__ double red[8][33];
   // locate this block's segment
   int blk = blockIdx.x, s = 0;
@@ -29,6 +27,9 @@ __global__ __launch_bounds__(256) void k_reduce_segments(const float* __restrict
   }
   if (s >= segs.n) return;
   const ReduceSegment& sg = segs.seg[s];
+  const float* __restrict__ part = sg.part;
+  const int64_t wstride = sg.wstride;
+  const int P = sg.P;
   const int eblocks = (sg.E + 31) / 32;
   const int eb = blk % eblocks;
   const int oh = (blk / eblocks) % sg.Ho;
@@ -61,18 +62,16 @@ __global__ __launch_bounds__(256) void k_reduce_segments(const float* __restrict
     double t = 0.0;
 #pragma unroll
     for (int g = 0; g < 8; ++g) t += red[g][el];
-    sg.out[((int64_t)ob * sg.Ho + oh) * sg.E + e] = (float)(t * sg.scale);
+    sg.out[((int64_t)ob * sg.Ho + oh) * sg.E + e] = (float)t;
   }
 }
 
-hipError_t launch_reduce(const float* part, int64_t wave_stride, int B, int H, int P,
-                         const ReduceSegments& segs, hipStream_t st) {
+hipError_t launch_reduce(int B, int H, const ReduceSegments& segs, hipStream_t st) {
   int64_t blocks = 0;
   for (int s = 0; s < segs.n; ++s)
     blocks += (int64_t)((segs.seg[s].E + 31) / 32) * segs.seg[s].Bo * segs.seg[s].Ho;
   if (blocks <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_reduce_segments, dim3((unsigned)blocks), dim3(256), 0, st, part,
-                     wave_stride, B, H, P, segs);
+  hipLaunchKernelGGL(k_reduce_segments, dim3((unsigned)blocks), dim3(256), 0, st, B, H, segs);
   return hipGetLastError();
 }
 

@@ -1,0 +1,165 @@
+// Per-tile building blocks shared by the whole-G and the G-blocked kernels:
+// logits on MFMA, the softmax over slots of a point pair, the softmax
+// Jacobian, and row loads/stores of (B, N, H, C) point tensors.
+#pragma once
+#include "fs_device.h"
+#include "fs_internal.h"
+
+namespace fs {
+
+// Logits of slots that do not exist (g >= G): finite and far below any real
+// logit, so exp2 gives exactly 0 and 0 * (t2 - m2) stays 0.
+constexpr float kNoSlot = -1e30f;
+
+// DK: 0 = every dot fp32 MFMA; 1 = value dots bf16 (reference level 2,
+// "bf16v"); 2 = every dot bf16 (level 3).
+template <int DK> struct Modes {
+  static constexpr int L = (DK == 2) ? MMA_BF16 : MMA_F32;
+  static constexpr int V = (DK >= 1) ? MMA_BF16 : MMA_F32;
+};
+
+// Scaled logits t2 = (x . W + b) * log2(e) / tau of one tile, as
+// [point-outer, slot-inner] fragments.
+template <int ML, int NGB, int NDB>
+__device__ __forceinline__ void logits_tile(float (&t2)[NGB][16], const float (&wA)[NGB][NDB][16],
+                                            const float (&xf)[NDB][16], const float (&bc)[NGB][16],
+                                            float cst) {
+#pragma unroll
+  for (int gb = 0; gb < NGB; ++gb) {
+    f32x16 s = zero16();
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) s = mma32<ML>(wA[gb][db], xf[db], s);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) t2[gb][r] = fmaf(s[r], cst, bc[gb][r]);
+  }
+}
+
+// Softmax over the G slots of each point (lane pair c, c + 32 holds one
+// point). Returns w (zero for points beyond N), the row max m2 (log2 units)
+// and the row sum. The row sum is formed in a fixed order (lane-local, then
+// the partner), so both lanes of a pair hold the same value.
+template <int NGB>
+__device__ __forceinline__ void softmax_tile(float (&w)[NGB][16], float& m2, float& lsum,
+                                             const float (&t2)[NGB][16], bool pv) {
+  float m = -INFINITY;
+#pragma unroll
+  for (int gb = 0; gb < NGB; ++gb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) m = fmaxf(m, t2[gb][r]);
+  m = fmaxf(m, xor32(m));
+  float l = 0.f;
+#pragma unroll
+  for (int gb = 0; gb < NGB; ++gb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float e = __builtin_amdgcn_exp2f(t2[gb][r] - m);
+      w[gb][r] = e;
+      l += e;
+    }
+  l += xor32(l);
+  const float inv = pv ? 1.f / l : 0.f;  // correctly rounded (no fast-math)
+#pragma unroll
+  for (int gb = 0; gb < NGB; ++gb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) w[gb][r] *= inv;
+  m2 = m;
+  lsum = l;
+}
+
+// The row max as consumers of saved statistics reconstruct it: stored in
+// natural units (m = m2 ln 2) and read back as m * log2(e). A row sum that is
+// to normalise weights formed against that value must be taken against it
+// too, or every weight of the row carries the same relative error
+// 2^(m2 - m2') and the row stops summing to one.
+__device__ __forceinline__ float stats_max_roundtrip(float m2) { return (m2 * kLn2) * kLog2e; }
+
+// Softmax statistics of one point in the reference layout (B, H, 2, N):
+// the row max of the natural-unit logits and the sum of exponentials
+// against the max consumers will read back (reference blocked.py:1329-1335).
+// `l` is the sum against `m2`; it is rescaled once to the round-tripped max.
+// Written by lane h = 0 of each pair.
+// `l_roundtrip`: l is already the sum against stats_max_roundtrip(m2).
+__device__ __forceinline__ void store_stats(float* stats, int bh, int N, int p, bool pv, int h,
+                                            float m2, float l, bool l_roundtrip = false) {
+  if (stats && pv && h == 0) {
+    float* base = stats + (int64_t)bh * 2 * N;
+    base[p] = m2 * kLn2;
+    base[N + p] = l_roundtrip ? l : l * __builtin_amdgcn_exp2f(m2 - stats_max_roundtrip(m2));
+  }
+}
+
+// The softmax Jacobian of one tile given omega = dL/dw: Lb = w (omega -
+// delta), delta = sum_g w omega, both from the same rounded products.
+// Overwrites om with ab = Lb / tau and returns the row term
+// sum_g Lb (t2 - m2) of the temperature gradient (natural units up to a
+// factor ln 2; zero on lanes h = 1 and on points beyond N). Shifting the
+// logits by the row max is exact in real arithmetic (sum_g Lb = 0) and
+// keeps the terms small.
+template <int NGB>
+__device__ __forceinline__ float jacobian_tile(float (&om)[NGB][16], const float (&w)[NGB][16],
+                                               const float (&t2)[NGB][16], float m2,
+                                               float inv_tau, bool pv, int h) {
+  float d = 0.f;
+#pragma unroll
+  for (int gb = 0; gb < NGB; ++gb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) d += w[gb][r] * om[gb][r];
+  d += xor32(d);
+  float rt = 0.f;
+#pragma unroll
+  for (int gb = 0; gb < NGB; ++gb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float lb = w[gb][r] * (om[gb][r] - d);
+      rt = fmaf(lb, t2[gb][r] - m2, rt);
+      om[gb][r] = lb * inv_tau;
+    }
+  rt += xor32(rt);
+  return (pv && h == 0) ? rt : 0.f;
+}
+
+// A 32-point tile's [point-outer, column-inner] fragments of one (B, N, H, C)
+// tensor: the fast form on full aligned rows (row clamped to N - 1), the
+// masked form otherwise.
+template <typename T, int NB>
+__device__ __forceinline__ void load_rows(float (&f)[NB][16], const T* base, int64_t sn, int p,
+                                          int N, int C, bool fast, bool vec, int h) {
+  if (fast) {
+    const T* row = base + (int64_t)(p < N ? p : N - 1) * sn;
+#pragma unroll
+    for (int k = 0; k < NB; ++k) load_frag_rows_fast<T>(f[k], row, 32 * k, h);
+  } else {
+    const T* row = base + (int64_t)p * sn;
+#pragma unroll
+    for (int k = 0; k < NB; ++k) load_frag_rows<T>(f[k], row, p < N, 32 * k, C, vec, h);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store_rows(T* row, const f32x16& v, bool pv, int c0, int C,
+                                           bool fast, bool vec, int h) {
+  if (fast) {
+    if (!pv) return;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      typename Vec4<T>::type o;
+      o[0] = from_f<T>(v[4 * q + 0]);
+      o[1] = from_f<T>(v[4 * q + 1]);
+      o[2] = from_f<T>(v[4 * q + 2]);
+      o[3] = from_f<T>(v[4 * q + 3]);
+      *reinterpret_cast<typename Vec4<T>::type*>(row + c0 + 8 * q + 4 * h) = o;
+    }
+  } else {
+    store_frag_rows<T>(row, v, pv, c0, C, vec, h);
+  }
+}
+
+template <typename T, int NB>
+__device__ __forceinline__ void copy_frags(float (&dst)[NB][16], const float (&src)[NB][16]) {
+#pragma unroll
+  for (int k = 0; k < NB; ++k)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) dst[k][j] = src[k][j];
+}
+
+}  // namespace fs

@@ -40,7 +40,7 @@ class FsSliceParams(ctypes.Structure):
                 ("bias", ctypes.c_void_p),
                 ("b_stride_b", ctypes.c_int64), ("b_stride_h", ctypes.c_int64),
                 ("tau", ctypes.c_void_p),
-                ("dot", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                ("dot", ctypes.c_int32), ("family", ctypes.c_int32)]
 
 
 class FlashSliceLibError(RuntimeError):

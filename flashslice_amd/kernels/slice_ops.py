@@ -263,10 +263,13 @@ class _Call:
             raise ValueError("tau must have H=%d elements, got %d" % (H, self.tau.numel()))
         swb, swh, sbb, sbh = _wb_layout(self.weight, self.bias, B, H)
         G = self.weight.shape[-2]
+        # kernel mode 'blocked' also forces the G-blocked HIP kernels, so
+        # both families can be held to the same gates on any shape
+        family = 2 if _KERNEL_MODE == "blocked" else 0
         self.prm = _hip.FsSliceParams(B, N, H, D, dv, G,
                                       self.weight.data_ptr(), swb, swh,
                                       self.bias.data_ptr(), sbb, sbh,
-                                      self.tau.data_ptr(), int(dot), 0)
+                                      self.tau.data_ptr(), int(dot), family)
         self.B, self.N, self.H, self.D, self.DV, self.G = B, N, H, D, dv, G
 
     def workspace(self, op):

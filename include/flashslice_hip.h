@@ -73,7 +73,7 @@ typedef struct fs_slice_params {
   int64_t b_stride_b, b_stride_h;       /* 0 where shared */
   const float* tau;                     /* (H,) fp32 */
   int32_t dot;                          /* 0 ieee, 1 tf32, 2 bf16v, 3 bf16, 4 tf32x3 */
-  int32_t reserved;
+  int32_t family;                       /* 0 auto, 1 whole-G where it fits, 2 G-blocked */
 } fs_slice_params;
 
 /* Bytes of workspace an op needs for this shape (op: enum fs_op). */
@@ -120,8 +120,10 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
                        float* dtokens, float* dweight, float* dbias, float* dtau,
                        void* workspace, size_t workspace_bytes, void* stream);
 
-/* Which kernel family serves this shape and dot level: 1 = whole-G (the
- * slot axis held in registers, one pass per op), 2 = G-blocked. */
+/* Which kernel family serves this call: 1 = whole-G (the slot axis held in
+ * registers, one pass per op; chosen where the shape fits, G <= 128 and
+ * D, DV small enough), 2 = G-blocked (any G: per-point softmax statistics,
+ * point-owned and slot-owned kernels). p->family = 2 forces G-blocked. */
 int32_t fs_family(const fs_slice_params* p);
 
 /* Text of the last error on the calling thread ("" if none). */
