@@ -1,0 +1,137 @@
+"""The custom-operator boundary on the CPU (no kernel runs).
+
+* the eight ``torch.ops.flashslice`` ops exist with the reference's schemas
+  (reference ``slice_ops.py:787-801``, ``blocked.py:1477-1494``);
+* their fake (meta) implementations give every output's shape and dtype
+  (reference ``slice_ops.py:894-919``, ``blocked.py:1502-1529``);
+* they are registered for the CUDA dispatch key only: a CPU tensor raises,
+  there is no CPU fallback;
+* ``torch.compile`` sees them as single opaque nodes (traced on meta
+  tensors).
+"""
+
+import pytest
+import torch
+
+import flashslice_amd.kernels  # noqa: F401  -- registers the ops
+
+SCHEMAS = {
+    "flash_slice": "flash_slice(Tensor x_mid, Tensor fx_mid, Tensor weight, Tensor bias, "
+                   "Tensor tau, int dot) -> (Tensor, Tensor)",
+    "flash_slice_bwd": "flash_slice_bwd(Tensor x_mid, Tensor fx_mid, Tensor weight, "
+                       "Tensor bias, Tensor tau, Tensor dz_num, Tensor ds, int dot) -> "
+                       "(Tensor, Tensor, Tensor, Tensor, Tensor)",
+    "flash_deslice": "flash_deslice(Tensor x_mid, Tensor weight, Tensor bias, Tensor tau, "
+                     "Tensor tokens, int dot) -> Tensor",
+    "flash_deslice_bwd": "flash_deslice_bwd(Tensor x_mid, Tensor weight, Tensor bias, "
+                         "Tensor tau, Tensor tokens, Tensor d_out, int dot) -> "
+                         "(Tensor, Tensor, Tensor, Tensor, Tensor)",
+    "slice_blk": "slice_blk(Tensor x_mid, Tensor fx_mid, Tensor weight, Tensor bias, "
+                 "Tensor tau, Tensor? stats, int dot) -> (Tensor, Tensor, Tensor)",
+    "slice_blk_bwd": "slice_blk_bwd(Tensor x_mid, Tensor fx_mid, Tensor weight, Tensor bias, "
+                     "Tensor tau, Tensor stats, Tensor dz_num, Tensor ds, int dot) -> "
+                     "(Tensor, Tensor, Tensor, Tensor, Tensor)",
+    "deslice_blk": "deslice_blk(Tensor x_mid, Tensor weight, Tensor bias, Tensor tau, "
+                   "Tensor tokens, Tensor? stats, int dot) -> (Tensor, Tensor)",
+    "deslice_blk_bwd": "deslice_blk_bwd(Tensor x_mid, Tensor weight, Tensor bias, Tensor tau, "
+                       "Tensor tokens, Tensor stats, Tensor d_out, int dot) -> "
+                       "(Tensor, Tensor, Tensor, Tensor, Tensor)",
+}
+
+
+def _norm(s):
+    return " ".join(s.replace("flashslice::", "").split())
+
+
+@pytest.mark.parametrize("name", sorted(SCHEMAS))
+def test_schema(name):
+    op = getattr(torch.ops.flashslice, name).default
+    assert _norm(str(op._schema)) == _norm(SCHEMAS[name])
+
+
+def _meta_inputs(B=2, N=37, H=3, D=8, DV=12, G=5):
+    m = lambda *s, dtype=torch.float32: torch.empty(*s, device="meta", dtype=dtype)  # noqa: E731
+    return dict(x=m(B, N, H, D, dtype=torch.bfloat16), fx=m(B, N, H, DV, dtype=torch.bfloat16),
+                w=m(H, G, D), b=m(H, G), tau=m(H), tok=m(B, H, G, DV),
+                dz=m(B, H, G, DV), ds=m(B, H, G), dout=m(B, N, H, DV, dtype=torch.bfloat16),
+                st=m(B, H, 2, N))
+
+
+def test_fake_shapes_and_dtypes():
+    t = _meta_inputs()
+    ops = torch.ops.flashslice
+    z, s = ops.flash_slice(t["x"], t["fx"], t["w"], t["b"], t["tau"], 0)
+    assert z.shape == (2, 3, 5, 12) and z.dtype == torch.float32
+    assert s.shape == (2, 3, 5) and s.dtype == torch.float32
+    out = ops.flash_deslice(t["x"], t["w"], t["b"], t["tau"], t["tok"], 0)
+    assert out.shape == (2, 37, 3, 12) and out.dtype == torch.bfloat16
+    g = ops.flash_slice_bwd(t["x"], t["fx"], t["w"], t["b"], t["tau"], t["dz"], t["ds"], 0)
+    assert [x.shape for x in g] == [t["x"].shape, t["fx"].shape, t["w"].shape, t["b"].shape,
+                                    t["tau"].shape]
+    assert [x.dtype for x in g] == [torch.bfloat16, torch.bfloat16] + [torch.float32] * 3
+    g = ops.flash_deslice_bwd(t["x"], t["w"], t["b"], t["tau"], t["tok"], t["dout"], 0)
+    assert [x.shape for x in g] == [t["x"].shape, t["tok"].shape, t["w"].shape, t["b"].shape,
+                                    t["tau"].shape]
+    z, s, st = ops.slice_blk(t["x"], t["fx"], t["w"], t["b"], t["tau"], None, 0)
+    assert st.shape == (2, 3, 2, 37) and st.dtype == torch.float32
+    out, st = ops.deslice_blk(t["x"], t["w"], t["b"], t["tau"], t["tok"], None, 0)
+    assert out.shape == (2, 37, 3, 12) and st.shape == (2, 3, 2, 37)
+    g = ops.slice_blk_bwd(t["x"], t["fx"], t["w"], t["b"], t["tau"], t["st"], t["dz"], t["ds"], 0)
+    assert len(g) == 5 and g[2].shape == t["w"].shape
+    g = ops.deslice_blk_bwd(t["x"], t["w"], t["b"], t["tau"], t["tok"], t["st"], t["dout"], 0)
+    assert len(g) == 5 and g[1].shape == t["tok"].shape
+
+
+def test_no_cpu_fallback():
+    """The ops have only a CUDA-key (HIP) implementation: CPU tensors raise
+    instead of silently running some other code."""
+    x = torch.randn(1, 8, 2, 4)
+    w, b, tau = torch.randn(3, 4), torch.zeros(3), torch.ones(2)
+    with pytest.raises(NotImplementedError):
+        torch.ops.flashslice.flash_slice(x, x, w, b, tau, 0)
+    with pytest.raises(NotImplementedError):
+        torch.ops.flashslice.deslice_blk(x, w, b, tau, torch.randn(1, 2, 3, 4), None, 0)
+
+
+def test_autograd_registered():
+    """setup_context saves inputs; the forward on meta tensors records an
+    autograd node whose backward is the registered formula (shape-checked
+    through the fakes)."""
+    B, N, H, D, G = 1, 16, 2, 4, 3
+    x = torch.empty(B, N, H, D, device="meta", requires_grad=True)
+    fx = torch.empty(B, N, H, D, device="meta", requires_grad=True)
+    w = torch.empty(G, D, device="meta", requires_grad=True)
+    b = torch.empty(G, device="meta", requires_grad=True)
+    tau = torch.empty(H, device="meta", requires_grad=True)
+    z, s = torch.ops.flashslice.flash_slice(x, fx, w, b, tau, 0)
+    assert z.grad_fn is not None
+    gx, gfx, gw, gb, gt = torch.autograd.grad((z.sum() + s.sum()), [x, fx, w, b, tau])
+    assert gx.shape == x.shape and gw.shape == w.shape and gt.shape == tau.shape
+    tok = torch.empty(B, H, G, D, device="meta", requires_grad=True)
+    out = torch.ops.flashslice.flash_deslice(x, w, b, tau, tok, 0)
+    gs = torch.autograd.grad(out.sum(), [x, w, b, tau, tok])
+    assert [g.shape for g in gs] == [x.shape, w.shape, b.shape, tau.shape, tok.shape]
+    z, s, st = torch.ops.flashslice.slice_blk(x, fx, w, b, tau, None, 0)
+    gs = torch.autograd.grad(z.sum(), [x, fx, w, b, tau])
+    assert gs[0].shape == x.shape
+
+
+def test_compile_keeps_one_graph():
+    """torch.compile traces the public API into a single graph with the ops
+    as opaque nodes (no graph breaks); traced on meta tensors so that no
+    kernel runs."""
+    import torch._dynamo
+    from flashslice_amd.kernels import fused_deslice, fused_slice
+
+    def coupling(x, fx, w, b, tau):
+        z, s, st = fused_slice(x, fx, w, b, tau, return_stats=True)
+        tok = z / (s + 1e-5)[..., None]
+        return fused_deslice(x, w, b, tau, tok, stats=st)
+
+    torch._dynamo.reset()
+    t = _meta_inputs(D=8, DV=8, G=8)
+    x32 = torch.empty(2, 37, 3, 8, device="meta")
+    explain = torch._dynamo.explain(coupling)(x32, x32, t["w"][:, :, :8].contiguous(),
+                                              t["b"], t["tau"])
+    assert explain.graph_break_count == 0, explain.break_reasons
+    assert explain.graph_count == 1
