@@ -207,7 +207,9 @@ __global__ __launch_bounds__(256, 2) void k_blk_stats(Args a) {
 template <typename T, int DK, int NB, bool ONLINE>
 __global__ __launch_bounds__(256, 2) void k_blk_deslice(Args a) {
   constexpr int ML = Modes<DK>::L, MV = Modes<DK>::V;
+  __shared__ float smem_rows[kWavesPerBlock * 32];
   BK_PROLOGUE
+  float* lds_x = smem_rows + wid * 32;
   const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
   T* ob = (T*)a.o1 + b * a.s1b + hd * a.s1h;
   const float* Tp = a.tok + (int64_t)bh * G * DV;
@@ -245,10 +247,13 @@ __global__ __launch_bounds__(256, 2) void k_blk_deslice(Args a) {
         sb += xor32(sb);
         l = l * alpha + sb;
         m2 = mb;
+        // acc is [v-outer, point-inner]: rescale register r by its point's alpha
+        float alpha_r[16];
+        gather_rows(alpha_r, alpha, lds_x, c, h);
 #pragma unroll
         for (int k = 0; k < NB; ++k)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[k][r] *= alpha;
+          for (int r = 0; r < 16; ++r) acc[k][r] *= alpha_r[r];
       } else {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -260,18 +265,21 @@ __global__ __launch_bounds__(256, 2) void k_blk_deslice(Args a) {
       blk_colouter<NB>(tc, Tp, 32 * gb, G, DV, nv, c, h);
 #pragma unroll
       for (int k = 0; k < NB; ++k)
-        if (k < nv) acc[k] = mma32<MV>(tc[k], e, acc[k]);
+        if (k < nv) acc[k] = mma32<MV>(e, tc[k], acc[k]);
     }
     if (!ONLINE) l = lown + xor32(lown);
+    // acc is [v-outer, point-inner]: point kmap(r, h)'s row sum lives on the
+    // lanes holding that point, so gather it by register from the pair
     const float inv_l = 1.f / l;
-    T* orow = ob + (int64_t)p * a.s1n;
+    float inv_r[16];
+    gather_rows(inv_r, inv_l, lds_x, c, h);
 #pragma unroll
     for (int k = 0; k < NB; ++k)
       if (k < nv) {
         f32x16 o = acc[k];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[r] *= inv_l;
-        store_rows<T>(orow, o, pv, 32 * k, DV, fast, a.vec_1, h);
+        for (int r = 0; r < 16; ++r) o[r] *= inv_r[r];
+        store_cols<T>(ob, a.s1n, o, t * kTile, N, 32 * k, DV, c, h);
       }
     if (ONLINE) store_stats(a.stats_out, bh, N, p, pv, h, m2, l);
   }
@@ -351,7 +359,9 @@ __global__ __launch_bounds__(256, 2) void k_blk_slice_g(Args a) {
 template <typename T, int DK, int NB, bool SLICE>
 __global__ __launch_bounds__(256, 2) void k_blk_bwd_n(Args a) {
   constexpr int ML = Modes<DK>::L, MV = Modes<DK>::V;
+  __shared__ float smem_rows[kWavesPerBlock * 32];
   BK_PROLOGUE
+  float* lds_x = smem_rows + wid * 32;
   const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
   const T* fb = (const T*)a.f + b * a.sfb + hd * a.sfh;
   T* dxb = (T*)a.o1 + b * a.s1b + hd * a.s1h;
@@ -390,7 +400,7 @@ __global__ __launch_bounds__(256, 2) void k_blk_bwd_n(Args a) {
         blk_colouter<NB>(zc, Zp, 32 * gb, G, DV, nv, c, h);
 #pragma unroll
         for (int k = 0; k < NB; ++k)
-          if (k < nv) dfacc[k] = mma32<MV>(zc[k], e, dfacc[k]);
+          if (k < nv) dfacc[k] = mma32<MV>(e, zc[k], dfacc[k]);
       }
       float zr[NB][16];
       blk_rowouter<NB>(zr, Zp, 32 * gb, G, DV, nv, c, h);
@@ -412,13 +422,16 @@ __global__ __launch_bounds__(256, 2) void k_blk_bwd_n(Args a) {
       a.lsum[(int64_t)bh * N + p] = l;
     }
     if (SLICE) {
+      // dfx is [v-outer, point-inner]: scale register r by its point's 1/l
+      float inv_r[16];
+      gather_rows(inv_r, inv_l, lds_x, c, h);
 #pragma unroll
       for (int k = 0; k < NB; ++k)
         if (k < nv) {
           f32x16 o = dfacc[k];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) o[r] *= inv_l;
-          store_rows<T>(dfb + (int64_t)p * a.s2n, o, pv, 32 * k, DV, fast, a.vec_2, h);
+          for (int r = 0; r < 16; ++r) o[r] *= inv_r[r];
+          store_cols<T>(dfb, a.s2n, o, t * kTile, N, 32 * k, DV, c, h);
         }
     }
     // pass 2
@@ -451,7 +464,7 @@ __global__ __launch_bounds__(256, 2) void k_blk_bwd_n(Args a) {
       blk_colouter<NB>(wc, Wp, 32 * gb, G, D, nd, c, h);
 #pragma unroll
       for (int k = 0; k < NB; ++k)
-        if (k < nd) dxacc[k] = mma32<MV>(wc[k], dl, dxacc[k]);
+        if (k < nd) dxacc[k] = mma32<MV>(dl, wc[k], dxacc[k]);
     }
 #pragma unroll
     for (int k = 0; k < NB; ++k)
@@ -459,7 +472,7 @@ __global__ __launch_bounds__(256, 2) void k_blk_bwd_n(Args a) {
         f32x16 o = dxacc[k];
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[r] *= inv_tau;
-        store_rows<T>(dxb + (int64_t)p * a.s1n, o, pv, 32 * k, D, fast, a.vec_1, h);
+        store_cols<T>(dxb, a.s1n, o, t * kTile, N, 32 * k, D, c, h);
       }
     rt += xor32(rt);
     dtacc += (pv && h == 0) ? rt : 0.f;

@@ -177,13 +177,13 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_fwd(Args a) {
     logits_tile<ML, NGB, NDB>(t2, wA, xf, bc, cst);
     softmax_tile<NGB>(w, m2, lsum, t2, pv);
     store_stats(a.stats_out, bh, N, p, pv, h, m2, lsum);
-    T* orow = ob + (int64_t)p * a.s1n;
+    // out as [v-outer, point-inner]: whole-row stores
 #pragma unroll
     for (int vb = 0; vb < NVB; ++vb) {
       f32x16 o = zero16();
 #pragma unroll
-      for (int gb = 0; gb < NGB; ++gb) o = mma32<MV>(tC[vb][gb], w[gb], o);
-      store_rows<T>(orow, o, pv, 32 * vb, DV, fast, a.vec_1, h);
+      for (int gb = 0; gb < NGB; ++gb) o = mma32<MV>(w[gb], tC[vb][gb], o);
+      store_cols<T>(ob, a.s1n, o, t * kTile, N, 32 * vb, DV, c, h);
     }
   }
 }
@@ -241,9 +241,9 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
       for (int gb = 0; gb < NGB; ++gb) {
         float zc[16];
         lds_frag_colouter(zc, sV, SM::SV, 32 * gb, 32 * vb, c, h);
-        o = mma32<MV>(zc, w[gb], o);
+        o = mma32<MV>(w[gb], zc, o);
       }
-      store_rows<T>(dfb + (int64_t)p * a.s2n, o, pv, 32 * vb, DV, fast, a.vec_2, h);
+      store_cols<T>(dfb, a.s2n, o, t * kTile, N, 32 * vb, DV, c, h);
     }
     // omega = fx . dz_num + ds
     float om[NGB][16];
@@ -268,9 +268,9 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
       for (int gb = 0; gb < NGB; ++gb) {
         float wc[16];
         lds_frag_colouter(wc, sW, SM::SW, 32 * gb, 32 * db, c, h);
-        o = mma32<MV>(wc, om[gb], o);
+        o = mma32<MV>(om[gb], wc, o);
       }
-      store_rows<T>(dxb + (int64_t)p * a.s1n, o, pv, 32 * db, D, fast, a.vec_1, h);
+      store_cols<T>(dxb, a.s1n, o, t * kTile, N, 32 * db, D, c, h);
     }
     // dW += ab^T x, db += sum_n ab
     float xT[NDB][16];
@@ -377,9 +377,9 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_bwd(Args a) {
       for (int gb = 0; gb < NGB; ++gb) {
         float wc[16];
         lds_frag_colouter(wc, sW, SM::SW, 32 * gb, 32 * db, c, h);
-        o = mma32<MV>(wc, om[gb], o);
+        o = mma32<MV>(om[gb], wc, o);
       }
-      store_rows<T>(dxb + (int64_t)p * a.s1n, o, pv, 32 * db, D, fast, a.vec_1, h);
+      store_cols<T>(dxb, a.s1n, o, t * kTile, N, 32 * db, D, c, h);
     }
     float xT[NDB][16];
 #pragma unroll

@@ -154,6 +154,43 @@ __device__ __forceinline__ void store_rows(T* row, const f32x16& v, bool pv, int
   }
 }
 
+// A per-point value held by the lane pair of each point (c, both h) as the
+// 16 values of a [column-outer, point-inner] fragment: o[r] = value of point
+// kmap(r, h). Through a 32-float wave-private LDS slot.
+__device__ __forceinline__ void gather_rows(float (&o)[16], float v, float* lds, int c, int h) {
+  __builtin_amdgcn_wave_barrier();
+  if (h == 0) lds[c] = v;
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 t = *reinterpret_cast<const float4*>(lds + 8 * q + 4 * h);
+    o[4 * q + 0] = t.x;
+    o[4 * q + 1] = t.y;
+    o[4 * q + 2] = t.z;
+    o[4 * q + 3] = t.w;
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Store a [column-outer, point-inner] fragment of a (B, N, H, C) tensor:
+// lane (c, h) writes column c0 + c of points p0 + kmap(r, h), so every store
+// instruction writes two whole contiguous 32-column row segments (128 B in
+// fp32) -- the write pattern HBM streams at full rate. `base` points at
+// element (b, 0, head, 0). Points >= N and columns >= C are skipped.
+template <typename T>
+__device__ __forceinline__ void store_cols(T* base, int64_t sn, const f32x16& v, int p0, int N,
+                                           int c0, int C, int c, int h) {
+  const int col = c0 + c;
+  if (col >= C) return;
+  T* colp = base + col;
+  const int pb = p0 + 4 * h;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int p = pb + 8 * (r >> 2) + (r & 3);
+    if (p < N) colp[(int64_t)p * sn] = from_f<T>(v[r]);
+  }
+}
+
 template <typename T, int NB>
 __device__ __forceinline__ void copy_frags(float (&dst)[NB][16], const float (&src)[NB][16]) {
 #pragma unroll
