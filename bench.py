@@ -151,6 +151,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="before the warmup, copy x once (B*N*H*D*4 bytes read and written): "
+                         "a kernel of known traffic that calibrates rocprofv3's FETCH_SIZE / "
+                         "WRITE_SIZE counters")
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
@@ -169,6 +173,14 @@ def main():
     torch.cuda.synchronize()
     print("[bench] %s; library %s" % (desc, _hip.lib().fs_version().decode()),
           file=sys.stderr, flush=True)
+
+    if a.copy_probe:
+        probe = torch.empty_like(inputs[0])
+        probe.copy_(inputs[0])
+        torch.cuda.synchronize()
+        print("[bench] copy probe: %d bytes read, %d written" % (
+            probe.numel() * 4, probe.numel() * 4), file=sys.stderr, flush=True)
+        del probe
 
     for _ in range(a.warmup):
         step_ops(*inputs)

@@ -98,6 +98,25 @@ int32_t check_points(const fs_points* t, const char* name, int64_t width, const 
   if (t->width != width)
     return fail(FS_ERR_INVALID, "%s: %s has width %d, expected %lld", who, name, t->width,
                 (long long)width);
+  // the kernels address a 32-point tile with 32-bit byte offsets from the
+  // tile's first row (fs_io.h)
+  const int64_t esz = t->dtype == fs::DT_F32 ? 4 : 2;
+  if (t->stride_b < 0 || t->stride_n < 0 || t->stride_h < 0)
+    return fail(FS_ERR_INVALID, "%s: %s has a negative stride", who, name);
+  if (t->stride_n * esz * fs::kTile >= (int64_t(1) << 30) ||
+      (int64_t)width * esz >= (int64_t(1) << 20))
+    return fail(FS_ERR_UNSUPPORTED, "%s: %s row stride %lld elements is too large", who, name,
+                (long long)t->stride_n);
+  return FS_OK;
+}
+// Outputs: rows must not overlap (a tile's stores of points >= N then fall
+// outside the range the kernels write through).
+int32_t check_out_points(const fs_points* t, const char* name, int64_t width, const char* who) {
+  const int32_t rc = check_points(t, name, width, who);
+  if (rc) return rc;
+  if (t->stride_n < width)
+    return fail(FS_ERR_INVALID, "%s: %s rows overlap (stride along N %lld < width %lld)", who,
+                name, (long long)t->stride_n, (long long)width);
   return FS_OK;
 }
 
@@ -344,7 +363,7 @@ int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float
   const char* who = "fs_deslice_fwd";
   int32_t rc = check_params(p, who);
   if (!rc) rc = check_points(x, "x_mid", p->D, who);
-  if (!rc) rc = check_points(out, "out", p->DV, who);
+  if (!rc) rc = check_out_points(out, "out", p->DV, who);
   if (rc) return rc;
   if (out->dtype != x->dtype) return fail(FS_ERR_INVALID, "%s: out and x_mid dtypes differ", who);
   if (!tokens) return fail(FS_ERR_INVALID, "%s: tokens is NULL", who);
@@ -386,8 +405,8 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
   int32_t rc = check_params(p, who);
   if (!rc) rc = check_points(x, "x_mid", p->D, who);
   if (!rc) rc = check_points(fx, "fx_mid", p->DV, who);
-  if (!rc) rc = check_points(dx, "dx", p->D, who);
-  if (!rc) rc = check_points(dfx, "dfx", p->DV, who);
+  if (!rc) rc = check_out_points(dx, "dx", p->D, who);
+  if (!rc) rc = check_out_points(dfx, "dfx", p->DV, who);
   if (rc) return rc;
   if (fx->dtype != x->dtype || dx->dtype != x->dtype || dfx->dtype != x->dtype)
     return fail(FS_ERR_INVALID, "%s: point tensors must share one dtype", who);
@@ -469,7 +488,7 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
   int32_t rc = check_params(p, who);
   if (!rc) rc = check_points(x, "x_mid", p->D, who);
   if (!rc) rc = check_points(d_out, "d_out", p->DV, who);
-  if (!rc) rc = check_points(dx, "dx", p->D, who);
+  if (!rc) rc = check_out_points(dx, "dx", p->D, who);
   if (rc) return rc;
   if (d_out->dtype != x->dtype || dx->dtype != x->dtype)
     return fail(FS_ERR_INVALID, "%s: point tensors must share one dtype", who);

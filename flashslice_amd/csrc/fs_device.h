@@ -38,7 +38,7 @@ constexpr float kLn2 = 0.6931471805599453f;
 // dot modes (reference slice_ops.py:338-343): 0 ieee, 1 tf32, 2 bf16v,
 // 3 bf16, 4 tf32x3. On gfx950 (no xf32 MFMA) levels 0/1/4 all run the
 // exact fp32 MFMA; 2 runs the value dots in bf16; 3 runs every dot in bf16.
-enum MmaMode { MMA_F32 = 0, MMA_BF16 = 1 };
+enum MmaMode { MMA_F32 = 0, MMA_BF16 = 1, MMA_X6 = 2 };
 
 __device__ __forceinline__ int kmap(int j, int h) { return 8 * (j >> 2) + 4 * h + (j & 3); }
 
@@ -197,6 +197,19 @@ __device__ __forceinline__ void lds_frag_colouter(float (&f)[16], const float* M
                                                   int c0, int c, int h) {
 #pragma unroll
   for (int j = 0; j < 16; ++j) f[j] = M[(r0 + kmap(j, h)) * S + c0 + c];
+}
+
+// A per-slot vector v[0..31] in LDS as lane half h's 16 values v[kmap(j, h)]
+// (four 16-byte reads; the 32 lanes of a half read the same words).
+__device__ __forceinline__ void lds_frag_vec(float (&f)[16], const float* v, int h) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 t = *reinterpret_cast<const float4*>(v + 8 * q + 4 * h);
+    f[4 * q + 0] = t.x;
+    f[4 * q + 1] = t.y;
+    f[4 * q + 2] = t.z;
+    f[4 * q + 3] = t.w;
+  }
 }
 
 // [a-outer, b-inner] -> [b-outer, a-inner] through a wave-private LDS tile

@@ -2,34 +2,53 @@
 //
 // A block is four waves working on the same (b, h): the block stages that
 // head's slice projection W (G x D) and its tokens / dz_num (G x DV) in LDS
-// once, and each wave owns one point partition pid = 4 * blockIdx.x + wave,
-// i.e. the strided tile sequence t = pid, pid + P, ... (a static
-// assignment, so per-wave partial sums are deterministic). The whole slot
-// axis G (padded to NGB blocks of 32) is held in registers, so the softmax
-// over G is exact in one pass and the N x H x G weight tensor never exists
-// outside registers. Every dot runs on MFMA: v_mfma_f32_32x32x2_f32 for the
-// ieee/tf32/tf32x3 levels and v_mfma_f32_32x32x16_bf16 for the bf16 levels
-// (fragment convention: fs_device.h). Slot-indexed sums (z_num, s,
-// dtokens, dW, db, dtau) are accumulated per wave and written as per-wave
-// partials that fs_reduce.hip sums in a fixed order. The next tile's point
-// rows are loaded while the current tile is computed.
+// once -- as the MFMA-ready operand fragments every tile reuses -- and each
+// wave owns one point partition pid = 4 * blockIdx.x + wave, i.e. the
+// strided tile sequence t = pid, pid + P, ... (a static assignment, so
+// per-wave partial sums are deterministic). The whole slot axis G (padded to
+// NGB blocks of 32) is held in registers, so the softmax over G is exact in
+// one pass and the N x H x G weight tensor never exists outside registers.
+// Every dot runs on the bf16 matrix cores (fs_mma.h): the ieee / tf32 /
+// tf32x3 levels as the exact three-piece split (MMA_X6, fp32-accurate), the
+// bf16 levels as plain bf16 MFMAs. Slot-indexed sums (z_num, s, dtokens, dW,
+// db, dtau) are accumulated per wave and written as per-wave partials that
+// fs_reduce.hip sums in a fixed order. The next tile's point rows are loaded
+// while the current tile is computed.
 //
 // Reference kernels these replace: _slice_fwd_kernel (slice_ops.py:554-599),
 // _deslice_fwd_kernel (:602-640), _slice_bwd_kernel (:643-710),
 // _deslice_bwd_kernel (:713-776).
 #pragma once
+#include <type_traits>
+
+#include "fs_mma.h"
 #include "fs_tile.h"
 
 namespace fs {
 
-// LDS of one block: W [32 NGB][SW], tokens / dz_num [32 NGB][SV] (row
-// strides padded so fragment reads are conflict-free), one transpose tile
-// per wave.
-template <int NGB, int NDB, int NVB> struct Smem {
+// MFMA modes of the whole-G kernels per dot kind DK: 0 = every dot fp32
+// accurate (MMA_X6); 1 = value dots bf16, logits fp32 accurate (reference
+// level 2, "bf16v"); 2 = every dot bf16 (level 3).
+template <int DK> struct FModes {
+  static constexpr int L = (DK == 2) ? MMA_BF16 : MMA_X6;
+  static constexpr int V = (DK >= 1) ? MMA_BF16 : MMA_X6;
+};
+
+// LDS of one block (floats): region 0 holds first the fp32 staging of W
+// [32 NGB][SW] and tokens / dz_num [32 NGB][SV] (row strides padded so
+// fragment reads are conflict-free) and, once the ready fragments are
+// built, the four per-wave transpose tiles; then NQL ready fragments of the
+// logits mode and NQV of the value mode; then two per-slot vectors (the
+// scaled bias, and d s in the slice backward).
+template <int NGB, int NDB, int NVB, int ML, int MV, int NQL, int NQV> struct FLds {
   static constexpr int GP = 32 * NGB;
   static constexpr int SW = 32 * NDB + 4, SV = 32 * NVB + 4;
-  static constexpr int W_OFF = 0, V_OFF = GP * SW, T_OFF = V_OFF + GP * SV;
-  static constexpr int TOTAL = T_OFF + kWavesPerBlock * kLdsTile;
+  static constexpr int STAGE = GP * SW + GP * SV, TILES = kWavesPerBlock * kLdsTile;
+  static constexpr int R0 = ((STAGE > TILES ? STAGE : TILES) + 3) / 4 * 4;
+  static constexpr int QL_OFF = R0;
+  static constexpr int QV_OFF = QL_OFF + NQL * frag_words<ML>() * 4;
+  static constexpr int VEC_OFF = QV_OFF + NQV * frag_words<MV>() * 4;  // bias * cst, ds
+  static constexpr int TOTAL = VEC_OFF + 2 * GP;
 };
 
 // Stage a small (G x C) fp32 matrix, zero-padded to (rows x cols), into LDS
@@ -42,46 +61,120 @@ __device__ __forceinline__ void stage_matrix(float* dst, int S, const float* src
   }
 }
 
+// Build n ready fragments of mode M into LDS (wave w builds i = w, w + 4,
+// ...); src(i, f) fills the fp32 fragment i from the staged matrices.
+template <int M, typename Src>
+__device__ __forceinline__ void build_frags(u32x4* dst, int n, int wid, int lane, Src&& src) {
+  for (int i = wid; i < n; i += kWavesPerBlock) {
+    float f[16];
+    src(i, f);
+    Frag<M> q;
+    prep<M>(q, f);
+    lds_put<M>(dst + i * frag_words<M>(), q, lane);
+  }
+}
+
 // Block prologue shared by the four kernels: head constants, LDS carve-up,
-// and the logits operands (W as the A operand [g-outer, d-inner] in
-// registers, bias * log2(e) / tau per output slot, -inf on padded slots).
-#define FS_PROLOGUE(NGB, NDB, NVB)                                                  \
-  using SM = Smem<NGB, NDB, NVB>;                                                   \
-  __shared__ float smem[SM::TOTAL];                                                 \
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;                       \
+// the fp32 staging of W and tokens / dz_num, and the logits operand W
+// [g-outer, d-inner] as ready fragments qL[gb * NDB + db] (bias * log2(e) /
+// tau per output slot in LDS, -1e30 on padded slots). The kernel
+// builds its value-mode fragments next and then calls FS_PROLOGUE_END.
+#define FS_PROLOGUE(NGB, NDB, NVB, NQV)                                             \
+  constexpr int ML = FModes<DK>::L, MV = FModes<DK>::V;                             \
+  using SM = FLds<NGB, NDB, NVB, ML, MV, NGB * NDB, NQV>;                          \
+  __shared__ __attribute__((aligned(16))) float smem[SM::TOTAL];                    \
+  const int lane = threadIdx.x & 63;                                                \
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);                 \
   const int c = lane & 31, h = lane >> 5;                                           \
   const int bh = blockIdx.y;                                                        \
   const int b = bh / a.H, hd = bh - b * a.H;                                       \
   const int pid = blockIdx.x * kWavesPerBlock + wid;                                \
   const int G = a.G, D = a.D, DV = a.DV, N = a.N;                                   \
-  float* sW = smem + SM::W_OFF;                                                     \
-  float* sV = smem + SM::V_OFF;                                                     \
-  float* lds = smem + SM::T_OFF + wid * kLdsTile;                                   \
+  float* sW = smem;                                                                 \
+  float* sV = smem + SM::GP * SM::SW;                                               \
+  float* lds = smem + wid * kLdsTile;                                               \
+  u32x4* qL = reinterpret_cast<u32x4*>(smem + SM::QL_OFF);                          \
+  u32x4* qV = reinterpret_cast<u32x4*>(smem + SM::QV_OFF);                          \
+  float* sBC = smem + SM::VEC_OFF;                                                  \
+  float* sDS = sBC + SM::GP;                                                        \
+  constexpr int FWL = frag_words<ML>(), FWV = frag_words<MV>();                     \
   const float* Wp = a.W + b * a.swb + hd * a.swh;                                   \
   const float* Bp = a.bias + b * a.sbb + hd * a.sbh;                                \
   const float tauf = a.tau[hd];                                                     \
   const float cst = (float)(1.4426950408889634 / (double)tauf);                    \
   const float inv_tau = 1.f / tauf;                                                 \
   const bool fast = a.fast != 0;                                                    \
-  (void)inv_tau; (void)sV; (void)lds; (void)DV;                                     \
+  (void)inv_tau; (void)sV; (void)qV; (void)FWV; (void)DV; (void)sDS;               \
   stage_matrix(sW, SM::SW, Wp, G, D, SM::GP, 32 * NDB);                             \
+  for (int i = threadIdx.x; i < SM::GP; i += 256) sBC[i] = i < G ? Bp[i] * cst : kNoSlot; \
   if (a.tok) stage_matrix(sV, SM::SV, a.tok + (int64_t)bh * G * DV, G, DV, SM::GP, 32 * NVB); \
   __syncthreads();                                                                  \
-  float wA[NGB][NDB][16], bc[NGB][16];                                              \
+  build_frags<ML>(qL, NGB * NDB, wid, lane, [&](int i, float(&f)[16]) {             \
+    lds_frag_rowouter(f, sW, SM::SW, 32 * (i / NDB), 32 * (i % NDB), c, h);         \
+  });
+
+// The staged fp32 matrices are dead once every ready fragment is built: the
+// transpose tiles reuse their space.
+#define FS_PROLOGUE_END __syncthreads();
+
+// Scaled logits t2 = (x . W + b) * log2(e) / tau of one tile from the
+// prepared x fragments, as [point-outer, slot-inner] fragments.
+#define FS_LOGITS(T2, XQ)                                                           \
   _Pragma("unroll") for (int gb = 0; gb < NGB; ++gb) {                              \
-    _Pragma("unroll") for (int db = 0; db < NDB; ++db)                              \
-      lds_frag_rowouter(wA[gb][db], sW, SM::SW, 32 * gb, 32 * db, c, h);            \
-    _Pragma("unroll") for (int r = 0; r < 16; ++r) {                                \
-      const int g = 32 * gb + kmap(r, h);                                           \
-      bc[gb][r] = g < G ? Bp[g] * cst : kNoSlot;                                  \
+    f32x16 s_ = zero16();                                                           \
+    _Pragma("unroll") for (int db = 0; db < NDB; ++db) {                            \
+      Frag<ML> wq_;                                                                 \
+      lds_get<ML>(wq_, qL + (gb * NDB + db) * FWL, lane);                           \
+      s_ = mma<ML>(wq_, XQ[db], s_);                                                \
     }                                                                               \
+    float bc_[16];                                                                  \
+    lds_frag_vec(bc_, sBC + 32 * gb, h);                                            \
+    _Pragma("unroll") for (int r = 0; r < 16; ++r) T2[gb][r] = fmaf(s_[r], cst, bc_[r]); \
   }
+
+// Point slices of one (b, h): byte base, byte row stride and row width in
+// bytes of a (B, N, H, C) tensor with element strides (sb, sn, sh), and the
+// byte offset of this lane's row c inside a tile.
+#define FS_SLICE(NAME, PTR, SB, SN, SH, C)                                                \
+  const char* NAME##_b = (const char*)(PTR) + (b * (SB) + hd * (SH)) * (int64_t)sizeof(T); \
+  const int64_t NAME##_sn = (SN) * (int64_t)sizeof(T);                                    \
+  const int64_t NAME##_w = (int64_t)(C) * (int64_t)sizeof(T);                             \
+  const uint32_t NAME##_row = (uint32_t)(c * NAME##_sn);
+
+// The tile loop of every point-owned kernel: two register sets of point
+// rows alternate, each reloaded (two tiles ahead) right after the tile it
+// held is computed, so no registers are copied between iterations. The first
+// pass is peeled so that the loop is entered with the same memory operations
+// outstanding as on every back edge: the compiler then waits only for the
+// rows a tile needs, never for the stores still in flight. A load beyond the
+// last tile reads an empty range (zeros, no memory traffic).
+#define FS_TILE_LOOP(LOAD, BODY, A_ARGS, B_ARGS)                                          \
+  {                                                                                       \
+    int t_ = pid;                                                                         \
+    LOAD(A_ARGS, t_);                                                                     \
+    LOAD(B_ARGS, t_ + a.P);                                                               \
+    if (t_ < a.ntiles) {                                                                  \
+      BODY(A_ARGS, t_);                                                                   \
+      LOAD(A_ARGS, t_ + 2 * a.P);                                                         \
+      t_ += a.P;                                                                          \
+      while (t_ < a.ntiles) {                                                             \
+        BODY(B_ARGS, t_);                                                                 \
+        LOAD(B_ARGS, t_ + 2 * a.P);                                                       \
+        t_ += a.P;                                                                        \
+        if (t_ >= a.ntiles) break;                                                        \
+        BODY(A_ARGS, t_);                                                                 \
+        LOAD(A_ARGS, t_ + 2 * a.P);                                                       \
+        t_ += a.P;                                                                        \
+      }                                                                                   \
+    }                                                                                     \
+  }
+#define FS_ARGS2(X, Y) X, Y
 
 // ------------------------------------------------------------------ slice fwd
 template <typename T, int DK, int NGB, int NDB, int NVB>
 __global__ __launch_bounds__(256, 2) void k_fused_slice_fwd(Args a) {
-  constexpr int ML = Modes<DK>::L, MV = Modes<DK>::V;
-  FS_PROLOGUE(NGB, NDB, NVB)
+  FS_PROLOGUE(NGB, NDB, NVB, 0)
+  FS_PROLOGUE_END
   f32x16 zacc[NGB][NVB];
   float sacc[NGB];
 #pragma unroll
@@ -90,54 +183,62 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_fwd(Args a) {
 #pragma unroll
     for (int vb = 0; vb < NVB; ++vb) zacc[gb][vb] = zero16();
   }
-  const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
-  const T* fb = (const T*)a.f + b * a.sfb + hd * a.sfh;
-  // the next tile's operands are loaded while the current one is computed
-  float xn[NDB][16], fn[NVB][16];
-  auto load_tile = [&](int t) {
-    const int p0 = t * kTile;
-    load_rows<T, NDB>(xn, xb, a.sxn, p0 + c, N, D, fast, a.vec_x, h);
-    // fx as [v-outer, point-inner]: one coalesced row read per register
+  FS_SLICE(x, a.x, a.sxb, a.sxn, a.sxh, D)
+  FS_SLICE(f, a.f, a.sfb, a.sfn, a.sfh, DV)
+  (void)f_row;
+  uint32_t vcf[NVB];  // fx is read as [v-outer, point-inner]: whole-row loads
 #pragma unroll
-    for (int vb = 0; vb < NVB; ++vb)
+  for (int vb = 0; vb < NVB; ++vb) vcf[vb] = col_off<T>(vb, DV, f_sn, c, h);
+  const float* st_m = a.stats_out ? a.stats_out + (int64_t)bh * 2 * N : nullptr;
+  const float* st_l = st_m ? st_m + N : nullptr;
+  auto run = [&](auto fast_c) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
+    float xA[NDB][16], xB[NDB][16], fA[NVB][16], fB[NVB][16];
+    auto load = [&](float (&xn)[NDB][16], float (&fn)[NVB][16], int t) {
+      const int64_t p0 = (int64_t)t * kTile;
+      ld_rows<T, NDB, FAST>(xn, rows_rsrc(x_b, x_sn, x_w, p0, N), vrx, D, h);
+      const Rsrc rf = rows_rsrc(f_b, f_sn, f_w, p0, N);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int pj = p0 + kmap(j, h), v = 32 * vb + c;
-        if (fast)
-          fn[vb][j] = to_f<T>(fb[(int64_t)(pj < N ? pj : N - 1) * a.sfn + v]);
-        else
-          fn[vb][j] = (pj < N && v < DV) ? to_f<T>(fb[(int64_t)pj * a.sfn + v]) : 0.f;
+      for (int vb = 0; vb < NVB; ++vb) ld_cols<T>(fn[vb], rf, vcf[vb], (uint32_t)f_sn);
+    };
+    auto body = [&](const float (&xf)[NDB][16], const float (&fT)[NVB][16], int t) {
+      const int64_t p0 = (int64_t)t * kTile;
+      const bool pv = p0 + c < N;
+      float t2[NGB][16], w[NGB][16], m2, lsum;
+      {
+        Frag<ML> xq[NDB];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xf[db]);
+        FS_LOGITS(t2, xq)
       }
+      softmax_tile<NGB>(w, m2, lsum, t2, pv);
+      store_stats_tile(st_m, st_l, p0, N, c, h, m2, lsum);
+      Frag<MV> fq[NVB];
+#pragma unroll
+      for (int vb = 0; vb < NVB; ++vb) prep<MV>(fq[vb], fT[vb]);
+#pragma unroll
+      for (int gb = 0; gb < NGB; ++gb) {
+        float wT[16];
+        transpose32(wT, w[gb], lds, c, h);
+        Frag<MV> wq;
+        prep<MV>(wq, wT);
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) zacc[gb][vb] = mma<MV>(fq[vb], wq, zacc[gb][vb]);
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s += wT[j];
+        sacc[gb] += s;
+      }
+    };
+    FS_TILE_LOOP(load, body, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
   };
-  if (pid < a.ntiles) load_tile(pid);
-  for (int t = pid; t < a.ntiles; t += a.P) {
-    const int p = t * kTile + c;
-    const bool pv = p < N;
-    float xf[NDB][16], fT[NVB][16];
-    copy_frags<T, NDB>(xf, xn);
-    copy_frags<T, NVB>(fT, fn);
-    if (t + a.P < a.ntiles) load_tile(t + a.P);
-    float t2[NGB][16], w[NGB][16], m2, lsum;
-    logits_tile<ML, NGB, NDB>(t2, wA, xf, bc, cst);
-    softmax_tile<NGB>(w, m2, lsum, t2, pv);
-    store_stats(a.stats_out, bh, N, p, pv, h, m2, lsum);
-#pragma unroll
-    for (int gb = 0; gb < NGB; ++gb) {
-      float wT[16];
-      transpose32(wT, w[gb], lds, c, h);
-#pragma unroll
-      for (int vb = 0; vb < NVB; ++vb) zacc[gb][vb] = mma32<MV>(fT[vb], wT, zacc[gb][vb]);
-      float s = 0.f;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) s += wT[j];
-      sacc[gb] += s;
-    }
-  }
+  if (fast) run(std::true_type()); else run(std::false_type());
   float* pw = a.part + ((int64_t)bh * a.P + pid) * part_floats_slice_fwd(G, DV);
 #pragma unroll
   for (int gb = 0; gb < NGB; ++gb) {
     const int g = 32 * gb + c;
-    const float s = sacc[gb] + xor32(sacc[gb]);
+    const float s = pair_sum(sacc[gb]);
     if (g < G) {
 #pragma unroll
       for (int vb = 0; vb < NVB; ++vb)
@@ -154,56 +255,122 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_fwd(Args a) {
 // ---------------------------------------------------------------- deslice fwd
 template <typename T, int DK, int NGB, int NDB, int NVB>
 __global__ __launch_bounds__(256, 2) void k_fused_deslice_fwd(Args a) {
-  constexpr int ML = Modes<DK>::L, MV = Modes<DK>::V;
-  FS_PROLOGUE(NGB, NDB, NVB)
-  float tC[NVB][NGB][16];  // tokens as [v-outer, g-inner]
+  FS_PROLOGUE(NGB, NDB, NVB, NVB * NGB)
+  // tokens as [v-outer, g-inner]: qV[vb * NGB + gb]
+  build_frags<MV>(qV, NVB * NGB, wid, lane, [&](int i, float(&f)[16]) {
+    lds_frag_colouter(f, sV, SM::SV, 32 * (i % NGB), 32 * (i / NGB), c, h);
+  });
+  FS_PROLOGUE_END
+  FS_SLICE(x, a.x, a.sxb, a.sxn, a.sxh, D)
+  FS_SLICE(o, a.o1, a.s1b, a.s1n, a.s1h, DV)
+  (void)o_row;
+  uint32_t vco[NVB];  // out is written as [v-outer, point-inner]: whole-row stores
 #pragma unroll
-  for (int vb = 0; vb < NVB; ++vb)
+  for (int vb = 0; vb < NVB; ++vb) vco[vb] = col_off<T>(vb, DV, o_sn, c, h);
+  const float* st_m = a.stats_out ? a.stats_out + (int64_t)bh * 2 * N : nullptr;
+  const float* st_l = st_m ? st_m + N : nullptr;
+  auto run = [&](auto fast_c) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
+    float xA[NDB][16], xB[NDB][16];
+    auto load = [&](float (&xn)[NDB][16], int t) {
+      ld_rows<T, NDB, FAST>(xn, rows_rsrc(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
+    };
+    auto body = [&](const float (&xf)[NDB][16], int t) {
+      const int64_t p0 = (int64_t)t * kTile;
+      const bool pv = p0 + c < N;
+      float t2[NGB][16], w[NGB][16], m2, lsum;
+      {
+        Frag<ML> xq[NDB];
 #pragma unroll
-    for (int gb = 0; gb < NGB; ++gb)
-      lds_frag_colouter(tC[vb][gb], sV, SM::SV, 32 * gb, 32 * vb, c, h);
-  const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
-  T* ob = (T*)a.o1 + b * a.s1b + hd * a.s1h;
-  float xn[NDB][16];
-  if (pid < a.ntiles) load_rows<T, NDB>(xn, xb, a.sxn, pid * kTile + c, N, D, fast, a.vec_x, h);
-  for (int t = pid; t < a.ntiles; t += a.P) {
-    const int p = t * kTile + c;
-    const bool pv = p < N;
-    float xf[NDB][16];
-    copy_frags<T, NDB>(xf, xn);
-    if (t + a.P < a.ntiles)
-      load_rows<T, NDB>(xn, xb, a.sxn, (t + a.P) * kTile + c, N, D, fast, a.vec_x, h);
-    float t2[NGB][16], w[NGB][16], m2, lsum;
-    logits_tile<ML, NGB, NDB>(t2, wA, xf, bc, cst);
-    softmax_tile<NGB>(w, m2, lsum, t2, pv);
-    store_stats(a.stats_out, bh, N, p, pv, h, m2, lsum);
-    // out as [v-outer, point-inner]: whole-row stores
+        for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xf[db]);
+        FS_LOGITS(t2, xq)
+      }
+      softmax_tile<NGB>(w, m2, lsum, t2, pv);
+      store_stats_tile(st_m, st_l, p0, N, c, h, m2, lsum);
+      f32x16 o[NVB];
 #pragma unroll
-    for (int vb = 0; vb < NVB; ++vb) {
-      f32x16 o = zero16();
+      for (int vb = 0; vb < NVB; ++vb) o[vb] = zero16();
 #pragma unroll
-      for (int gb = 0; gb < NGB; ++gb) o = mma32<MV>(w[gb], tC[vb][gb], o);
-      store_cols<T>(ob, a.s1n, o, t * kTile, N, 32 * vb, DV, c, h);
-    }
-  }
+      for (int gb = 0; gb < NGB; ++gb) {
+        Frag<MV> wq;
+        prep<MV>(wq, w[gb]);
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) {
+          Frag<MV> tq;
+          lds_get<MV>(tq, qV + (vb * NGB + gb) * FWV, lane);
+          o[vb] = mma<MV>(wq, tq, o[vb]);
+        }
+      }
+      const Rsrc ro = rows_rsrc(o_b, o_sn, o_w, p0, N);
+#pragma unroll
+      for (int vb = 0; vb < NVB; ++vb) st_cols<T>(ro, vco[vb], (uint32_t)o_sn, o[vb]);
+    };
+    FS_TILE_LOOP(load, body, xA, xB)
+  };
+  if (fast) run(std::true_type()); else run(std::false_type());
 }
+
+// dx = ab W and dW += ab^T x, db += sum_n ab for the two backward kernels:
+// `om` holds ab = Lb / tau ([point-outer, slot-inner]); qWc the ready
+// fragments of W as [d-outer, g-inner] (index db * NGB + gb).
+#define FS_DX_DW(OM, QWC)                                                           \
+  {                                                                                 \
+    f32x16 o_[NDB];                                                                 \
+    _Pragma("unroll") for (int db = 0; db < NDB; ++db) o_[db] = zero16();           \
+    _Pragma("unroll") for (int gb = 0; gb < NGB; ++gb) {                            \
+      Frag<MV> aq_;                                                                 \
+      prep<MV>(aq_, OM[gb]);                                                        \
+      _Pragma("unroll") for (int db = 0; db < NDB; ++db) {                          \
+        Frag<MV> wq_;                                                               \
+        lds_get<MV>(wq_, QWC + (db * NGB + gb) * FWV, lane);                        \
+        o_[db] = mma<MV>(aq_, wq_, o_[db]);                                         \
+      }                                                                             \
+    }                                                                               \
+    const Rsrc rdx_ = rows_rsrc(dx_b, dx_sn, dx_w, p0, N);                          \
+    _Pragma("unroll") for (int db = 0; db < NDB; ++db)                              \
+      st_cols<T>(rdx_, vcx[db], (uint32_t)dx_sn, o_[db]);                           \
+  }                                                                                 \
+  {                                                                                 \
+    Frag<MV> xTq_[NDB];                                                             \
+    _Pragma("unroll") for (int db = 0; db < NDB; ++db) {                            \
+      float xT_[16];                                                                \
+      transpose32(xT_, xf[db], lds, c, h);                                          \
+      prep<MV>(xTq_[db], xT_);                                                      \
+    }                                                                               \
+    _Pragma("unroll") for (int gb = 0; gb < NGB; ++gb) {                            \
+      float aT_[16];                                                                \
+      transpose32(aT_, OM[gb], lds, c, h);                                          \
+      Frag<MV> aTq_;                                                                \
+      prep<MV>(aTq_, aT_);                                                          \
+      _Pragma("unroll") for (int db = 0; db < NDB; ++db)                            \
+        dW[gb][db] = mma<MV>(xTq_[db], aTq_, dW[gb][db]);                           \
+      float s_ = 0.f;                                                               \
+      _Pragma("unroll") for (int j = 0; j < 16; ++j) s_ += aT_[j];                  \
+      dbacc[gb] += s_;                                                              \
+    }                                                                               \
+  }
 
 // ------------------------------------------------------------------ slice bwd
 template <typename T, int DK, int NGB, int NDB, int NVB>
 __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
-  constexpr int ML = Modes<DK>::L, MV = Modes<DK>::V;
-  FS_PROLOGUE(NGB, NDB, NVB)
-  // sW holds W, sV holds dz_num; dz_num is read per tile as [g-outer,
-  // v-inner] (omega) and [v-outer, g-inner] (dfx), W as [d-outer, g-inner].
-  const float* Sp = a.ds + (int64_t)bh * G;
-  float dsv[NGB][16];  // d s per output slot
-#pragma unroll
-  for (int gb = 0; gb < NGB; ++gb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int g = 32 * gb + kmap(r, h);
-      dsv[gb][r] = g < G ? Sp[g] : 0.f;
-    }
+  FS_PROLOGUE(NGB, NDB, NVB, 2 * NGB * NVB + NDB * NGB)
+  // dz_num as [g-outer, v-inner] (omega, qZr[gb * NVB + vb]) and [v-outer,
+  // g-inner] (dfx, qZc[vb * NGB + gb]); W as [d-outer, g-inner] (dx).
+  u32x4* qZr = qV;
+  u32x4* qZc = qV + NGB * NVB * FWV;
+  u32x4* qWc = qV + 2 * NGB * NVB * FWV;
+  build_frags<MV>(qZr, NGB * NVB, wid, lane, [&](int i, float(&f)[16]) {
+    lds_frag_rowouter(f, sV, SM::SV, 32 * (i / NVB), 32 * (i % NVB), c, h);
+  });
+  build_frags<MV>(qZc, NVB * NGB, wid, lane, [&](int i, float(&f)[16]) {
+    lds_frag_colouter(f, sV, SM::SV, 32 * (i % NGB), 32 * (i / NGB), c, h);
+  });
+  build_frags<MV>(qWc, NDB * NGB, wid, lane, [&](int i, float(&f)[16]) {
+    lds_frag_colouter(f, sW, SM::SW, 32 * (i % NGB), 32 * (i / NGB), c, h);
+  });
+  for (int i = threadIdx.x; i < SM::GP; i += 256) sDS[i] = i < G ? a.ds[(int64_t)bh * G + i] : 0.f;
+  FS_PROLOGUE_END
   f32x16 dW[NGB][NDB];
   float dbacc[NGB], dtacc = 0.f;
 #pragma unroll
@@ -212,87 +379,94 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db) dW[gb][db] = zero16();
   }
-  const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
-  const T* fb = (const T*)a.f + b * a.sfb + hd * a.sfh;
-  T* dxb = (T*)a.o1 + b * a.s1b + hd * a.s1h;
-  T* dfb = (T*)a.o2 + b * a.s2b + hd * a.s2h;
-  float xn[NDB][16], fnx[NVB][16];
-  auto load_tile = [&](int t) {
-    const int p = t * kTile + c;
-    load_rows<T, NDB>(xn, xb, a.sxn, p, N, D, fast, a.vec_x, h);
-    load_rows<T, NVB>(fnx, fb, a.sfn, p, N, DV, fast, a.vec_f, h);
+  FS_SLICE(x, a.x, a.sxb, a.sxn, a.sxh, D)
+  FS_SLICE(f, a.f, a.sfb, a.sfn, a.sfh, DV)
+  FS_SLICE(dx, a.o1, a.s1b, a.s1n, a.s1h, D)
+  FS_SLICE(df, a.o2, a.s2b, a.s2n, a.s2h, DV)
+  (void)dx_row; (void)df_row;
+  uint32_t vcx[NDB], vcf[NVB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) vcx[db] = col_off<T>(db, D, dx_sn, c, h);
+#pragma unroll
+  for (int vb = 0; vb < NVB; ++vb) vcf[vb] = col_off<T>(vb, DV, df_sn, c, h);
+  auto run = [&](auto fast_c) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
+    const uint32_t vrf = FAST ? f_row + 4 * h * (uint32_t)sizeof(T) : f_row;
+    // x is double-buffered; fx is dead once omega is formed, so its one
+    // buffer is reloaded for the wave's next tile right there
+    float xA[NDB][16], xB[NDB][16], ff[NVB][16];
+    auto load = [&](float (&xn)[NDB][16], int t) {
+      ld_rows<T, NDB, FAST>(xn, rows_rsrc(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
+    };
+    auto load_f = [&](int t) {
+      ld_rows<T, NVB, FAST>(ff, rows_rsrc(f_b, f_sn, f_w, (int64_t)t * kTile, N), vrf, DV, h);
+    };
+    auto body = [&](const float (&xf)[NDB][16], int t) {
+      const int64_t p0 = (int64_t)t * kTile;
+      const bool pv = p0 + c < N;
+      float t2[NGB][16], w[NGB][16], m2, lsum;
+      {
+        Frag<ML> xq[NDB];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xf[db]);
+        FS_LOGITS(t2, xq)
+      }
+      softmax_tile<NGB>(w, m2, lsum, t2, pv);
+      // dfx = w dz_num
+      {
+        f32x16 o[NVB];
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) o[vb] = zero16();
+#pragma unroll
+        for (int gb = 0; gb < NGB; ++gb) {
+          Frag<MV> wq;
+          prep<MV>(wq, w[gb]);
+#pragma unroll
+          for (int vb = 0; vb < NVB; ++vb) {
+            Frag<MV> zq;
+            lds_get<MV>(zq, qZc + (vb * NGB + gb) * FWV, lane);
+            o[vb] = mma<MV>(wq, zq, o[vb]);
+          }
+        }
+        const Rsrc rdf = rows_rsrc(df_b, df_sn, df_w, p0, N);
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) st_cols<T>(rdf, vcf[vb], (uint32_t)df_sn, o[vb]);
+      }
+      // omega = fx . dz_num + ds
+      float om[NGB][16];
+      {
+        Frag<MV> fq[NVB];
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) prep<MV>(fq[vb], ff[vb]);
+#pragma unroll
+        for (int gb = 0; gb < NGB; ++gb) {
+          f32x16 o = zero16();
+#pragma unroll
+          for (int vb = 0; vb < NVB; ++vb) {
+            Frag<MV> zq;
+            lds_get<MV>(zq, qZr + (gb * NVB + vb) * FWV, lane);
+            o = mma<MV>(zq, fq[vb], o);
+          }
+          float dsv[16];  // d s per output slot
+          lds_frag_vec(dsv, sDS + 32 * gb, h);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) om[gb][r] = o[r] + dsv[r];
+        }
+      }
+      load_f(t + a.P);
+      dtacc += jacobian_tile<NGB>(om, w, t2, m2, inv_tau, pv, h);
+      FS_DX_DW(om, qWc)
+    };
+    load_f(pid);
+    FS_TILE_LOOP(load, body, xA, xB)
   };
-  if (pid < a.ntiles) load_tile(pid);
-  for (int t = pid; t < a.ntiles; t += a.P) {
-    const int p = t * kTile + c;
-    const bool pv = p < N;
-    float xf[NDB][16], ff[NVB][16];
-    copy_frags<T, NDB>(xf, xn);
-    copy_frags<T, NVB>(ff, fnx);
-    if (t + a.P < a.ntiles) load_tile(t + a.P);
-    float t2[NGB][16], w[NGB][16], m2, lsum;
-    logits_tile<ML, NGB, NDB>(t2, wA, xf, bc, cst);
-    softmax_tile<NGB>(w, m2, lsum, t2, pv);
-    // dfx = w dz_num
-#pragma unroll
-    for (int vb = 0; vb < NVB; ++vb) {
-      f32x16 o = zero16();
-#pragma unroll
-      for (int gb = 0; gb < NGB; ++gb) {
-        float zc[16];
-        lds_frag_colouter(zc, sV, SM::SV, 32 * gb, 32 * vb, c, h);
-        o = mma32<MV>(w[gb], zc, o);
-      }
-      store_cols<T>(dfb, a.s2n, o, t * kTile, N, 32 * vb, DV, c, h);
-    }
-    // omega = fx . dz_num + ds
-    float om[NGB][16];
-#pragma unroll
-    for (int gb = 0; gb < NGB; ++gb) {
-      f32x16 o = zero16();
-#pragma unroll
-      for (int vb = 0; vb < NVB; ++vb) {
-        float zr[16];
-        lds_frag_rowouter(zr, sV, SM::SV, 32 * gb, 32 * vb, c, h);
-        o = mma32<MV>(zr, ff[vb], o);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) om[gb][r] = o[r] + dsv[gb][r];
-    }
-    dtacc += jacobian_tile<NGB>(om, w, t2, m2, inv_tau, pv, h);
-    // dx = ab W
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      f32x16 o = zero16();
-#pragma unroll
-      for (int gb = 0; gb < NGB; ++gb) {
-        float wc[16];
-        lds_frag_colouter(wc, sW, SM::SW, 32 * gb, 32 * db, c, h);
-        o = mma32<MV>(om[gb], wc, o);
-      }
-      store_cols<T>(dxb, a.s1n, o, t * kTile, N, 32 * db, D, c, h);
-    }
-    // dW += ab^T x, db += sum_n ab
-    float xT[NDB][16];
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) transpose32(xT[db], xf[db], lds, c, h);
-#pragma unroll
-    for (int gb = 0; gb < NGB; ++gb) {
-      float aT[16];
-      transpose32(aT, om[gb], lds, c, h);
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) dW[gb][db] = mma32<MV>(xT[db], aT, dW[gb][db]);
-      float s = 0.f;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) s += aT[j];
-      dbacc[gb] += s;
-    }
-  }
+  if (fast) run(std::true_type()); else run(std::false_type());
   float* pw = a.part + ((int64_t)bh * a.P + pid) * part_floats_slice_bwd(G, D);
 #pragma unroll
   for (int gb = 0; gb < NGB; ++gb) {
     const int g = 32 * gb + c;
-    const float s = dbacc[gb] + xor32(dbacc[gb]);
+    const float s = pair_sum(dbacc[gb]);
     if (g < G) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
@@ -311,10 +485,18 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
 // ---------------------------------------------------------------- deslice bwd
 template <typename T, int DK, int NGB, int NDB, int NVB>
 __global__ __launch_bounds__(256, 2) void k_fused_deslice_bwd(Args a) {
-  constexpr int ML = Modes<DK>::L, MV = Modes<DK>::V;
-  FS_PROLOGUE(NGB, NDB, NVB)
-  // sW holds W (read as [d-outer, g-inner] for dx), sV the tokens (read as
-  // [g-outer, v-inner] for omega).
+  FS_PROLOGUE(NGB, NDB, NVB, NGB * NVB + NDB * NGB)
+  // tokens as [g-outer, v-inner] (omega, qTr[gb * NVB + vb]); W as [d-outer,
+  // g-inner] (dx).
+  u32x4* qTr = qV;
+  u32x4* qWc = qV + NGB * NVB * FWV;
+  build_frags<MV>(qTr, NGB * NVB, wid, lane, [&](int i, float(&f)[16]) {
+    lds_frag_rowouter(f, sV, SM::SV, 32 * (i / NVB), 32 * (i % NVB), c, h);
+  });
+  build_frags<MV>(qWc, NDB * NGB, wid, lane, [&](int i, float(&f)[16]) {
+    lds_frag_colouter(f, sW, SM::SW, 32 * (i % NGB), 32 * (i / NGB), c, h);
+  });
+  FS_PROLOGUE_END
   f32x16 dT[NGB][NVB], dW[NGB][NDB];
   float dbacc[NGB], dtacc = 0.f;
 #pragma unroll
@@ -325,83 +507,88 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_bwd(Args a) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db) dW[gb][db] = zero16();
   }
-  const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
-  const T* ob = (const T*)a.f + b * a.sfb + hd * a.sfh;
-  T* dxb = (T*)a.o1 + b * a.s1b + hd * a.s1h;
-  float xn[NDB][16], fnx[NVB][16];
-  auto load_tile = [&](int t) {
-    const int p = t * kTile + c;
-    load_rows<T, NDB>(xn, xb, a.sxn, p, N, D, fast, a.vec_x, h);
-    load_rows<T, NVB>(fnx, ob, a.sfn, p, N, DV, fast, a.vec_f, h);
+  FS_SLICE(x, a.x, a.sxb, a.sxn, a.sxh, D)
+  FS_SLICE(g, a.f, a.sfb, a.sfn, a.sfh, DV)
+  FS_SLICE(dx, a.o1, a.s1b, a.s1n, a.s1h, D)
+  (void)dx_row;
+  uint32_t vcx[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) vcx[db] = col_off<T>(db, D, dx_sn, c, h);
+  auto run = [&](auto fast_c) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
+    const uint32_t vrg = FAST ? g_row + 4 * h * (uint32_t)sizeof(T) : g_row;
+    // x is double-buffered; d_out is dead once omega is formed, so its one
+    // buffer is reloaded for the wave's next tile right there
+    float xA[NDB][16], xB[NDB][16], of[NVB][16];
+    auto load = [&](float (&xn)[NDB][16], int t) {
+      ld_rows<T, NDB, FAST>(xn, rows_rsrc(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
+    };
+    auto load_g = [&](int t) {
+      ld_rows<T, NVB, FAST>(of, rows_rsrc(g_b, g_sn, g_w, (int64_t)t * kTile, N), vrg, DV, h);
+    };
+    auto body = [&](const float (&xf)[NDB][16], int t) {
+      const int64_t p0 = (int64_t)t * kTile;
+      const bool pv = p0 + c < N;
+      float t2[NGB][16], w[NGB][16], m2, lsum;
+      {
+        Frag<ML> xq[NDB];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xf[db]);
+        FS_LOGITS(t2, xq)
+      }
+      softmax_tile<NGB>(w, m2, lsum, t2, pv);
+      // dtokens += w^T d_out (rows of d_out beyond N read as zero)
+      {
+        Frag<MV> oTq[NVB];
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) {
+          float oT[16];
+          transpose32(oT, of[vb], lds, c, h);
+          prep<MV>(oTq[vb], oT);
+        }
+#pragma unroll
+        for (int gb = 0; gb < NGB; ++gb) {
+          float wT[16];
+          transpose32(wT, w[gb], lds, c, h);
+          Frag<MV> wTq;
+          prep<MV>(wTq, wT);
+#pragma unroll
+          for (int vb = 0; vb < NVB; ++vb) dT[gb][vb] = mma<MV>(oTq[vb], wTq, dT[gb][vb]);
+        }
+      }
+      // omega = d_out . tokens
+      float om[NGB][16];
+      {
+        Frag<MV> oq[NVB];
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) prep<MV>(oq[vb], of[vb]);
+#pragma unroll
+        for (int gb = 0; gb < NGB; ++gb) {
+          f32x16 o = zero16();
+#pragma unroll
+          for (int vb = 0; vb < NVB; ++vb) {
+            Frag<MV> tq;
+            lds_get<MV>(tq, qTr + (gb * NVB + vb) * FWV, lane);
+            o = mma<MV>(tq, oq[vb], o);
+          }
+          from16(om[gb], o);
+        }
+      }
+      load_g(t + a.P);
+      dtacc += jacobian_tile<NGB>(om, w, t2, m2, inv_tau, pv, h);
+      FS_DX_DW(om, qWc)
+    };
+    load_g(pid);
+    FS_TILE_LOOP(load, body, xA, xB)
   };
-  if (pid < a.ntiles) load_tile(pid);
-  for (int t = pid; t < a.ntiles; t += a.P) {
-    const int p = t * kTile + c;
-    const bool pv = p < N;
-    float xf[NDB][16], of[NVB][16];
-    copy_frags<T, NDB>(xf, xn);
-    copy_frags<T, NVB>(of, fnx);
-    if (t + a.P < a.ntiles) load_tile(t + a.P);
-    float t2[NGB][16], w[NGB][16], m2, lsum;
-    logits_tile<ML, NGB, NDB>(t2, wA, xf, bc, cst);
-    softmax_tile<NGB>(w, m2, lsum, t2, pv);
-    // dtokens += w^T d_out (rows of d_out beyond N meet zero weights)
-    float oT[NVB][16];
-#pragma unroll
-    for (int vb = 0; vb < NVB; ++vb) transpose32(oT[vb], of[vb], lds, c, h);
-#pragma unroll
-    for (int gb = 0; gb < NGB; ++gb) {
-      float wT[16];
-      transpose32(wT, w[gb], lds, c, h);
-#pragma unroll
-      for (int vb = 0; vb < NVB; ++vb) dT[gb][vb] = mma32<MV>(oT[vb], wT, dT[gb][vb]);
-    }
-    // omega = d_out . tokens
-    float om[NGB][16];
-#pragma unroll
-    for (int gb = 0; gb < NGB; ++gb) {
-      f32x16 o = zero16();
-#pragma unroll
-      for (int vb = 0; vb < NVB; ++vb) {
-        float tr[16];
-        lds_frag_rowouter(tr, sV, SM::SV, 32 * gb, 32 * vb, c, h);
-        o = mma32<MV>(tr, of[vb], o);
-      }
-      from16(om[gb], o);
-    }
-    dtacc += jacobian_tile<NGB>(om, w, t2, m2, inv_tau, pv, h);
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      f32x16 o = zero16();
-#pragma unroll
-      for (int gb = 0; gb < NGB; ++gb) {
-        float wc[16];
-        lds_frag_colouter(wc, sW, SM::SW, 32 * gb, 32 * db, c, h);
-        o = mma32<MV>(om[gb], wc, o);
-      }
-      store_cols<T>(dxb, a.s1n, o, t * kTile, N, 32 * db, D, c, h);
-    }
-    float xT[NDB][16];
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) transpose32(xT[db], xf[db], lds, c, h);
-#pragma unroll
-    for (int gb = 0; gb < NGB; ++gb) {
-      float aT[16];
-      transpose32(aT, om[gb], lds, c, h);
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) dW[gb][db] = mma32<MV>(xT[db], aT, dW[gb][db]);
-      float s = 0.f;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) s += aT[j];
-      dbacc[gb] += s;
-    }
-  }
+  if (fast) run(std::true_type()); else run(std::false_type());
   float* pw = a.part + ((int64_t)bh * a.P + pid) * part_floats_deslice_bwd(G, D, DV);
   const int64_t offW = (int64_t)G * DV, offB = offW + (int64_t)G * D;
 #pragma unroll
   for (int gb = 0; gb < NGB; ++gb) {
     const int g = 32 * gb + c;
-    const float s = dbacc[gb] + xor32(dbacc[gb]);
+    const float s = pair_sum(dbacc[gb]);
     if (g < G) {
 #pragma unroll
       for (int vb = 0; vb < NVB; ++vb)

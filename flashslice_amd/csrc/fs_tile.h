@@ -4,6 +4,7 @@
 #pragma once
 #include "fs_device.h"
 #include "fs_internal.h"
+#include "fs_io.h"
 
 namespace fs {
 
@@ -46,7 +47,7 @@ __device__ __forceinline__ void softmax_tile(float (&w)[NGB][16], float& m2, flo
   for (int gb = 0; gb < NGB; ++gb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) m = fmaxf(m, t2[gb][r]);
-  m = fmaxf(m, xor32(m));
+  m = pair_max(m);
   float l = 0.f;
 #pragma unroll
   for (int gb = 0; gb < NGB; ++gb)
@@ -56,7 +57,7 @@ __device__ __forceinline__ void softmax_tile(float (&w)[NGB][16], float& m2, flo
       w[gb][r] = e;
       l += e;
     }
-  l += xor32(l);
+  l = pair_sum(l);
   const float inv = pv ? 1.f / l : 0.f;  // correctly rounded (no fast-math)
 #pragma unroll
   for (int gb = 0; gb < NGB; ++gb)
@@ -104,7 +105,7 @@ __device__ __forceinline__ float jacobian_tile(float (&om)[NGB][16], const float
   for (int gb = 0; gb < NGB; ++gb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) d += w[gb][r] * om[gb][r];
-  d += xor32(d);
+  d = pair_sum(d);
   float rt = 0.f;
 #pragma unroll
   for (int gb = 0; gb < NGB; ++gb)
@@ -114,8 +115,19 @@ __device__ __forceinline__ float jacobian_tile(float (&om)[NGB][16], const float
       rt = fmaf(lb, t2[gb][r] - m2, rt);
       om[gb][r] = lb * inv_tau;
     }
-  rt += xor32(rt);
+  rt = pair_sum(rt);
   return (pv && h == 0) ? rt : 0.f;
+}
+
+// store_stats for the tile loops that address points through buffer
+// resources: `sm` / `sl` are the max and sum rows of this (b, h) (null: no
+// statistics); points beyond N and lanes h = 1 store nothing.
+__device__ __forceinline__ void store_stats_tile(const float* sm, const float* sl, int64_t p0,
+                                                 int N, int c, int h, float m2, float l,
+                                                 bool l_roundtrip = false) {
+  st_pt(pts_rsrc(sm, p0, N), c, h, m2 * kLn2);
+  st_pt(pts_rsrc(sl, p0, N), c, h,
+        l_roundtrip ? l : l * __builtin_amdgcn_exp2f(m2 - stats_max_roundtrip(m2)));
 }
 
 // A 32-point tile's [point-outer, column-inner] fragments of one (B, N, H, C)

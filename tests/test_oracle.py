@@ -21,7 +21,15 @@ import torch
 
 import oracle
 
-torch.set_default_dtype(torch.float64)
+
+@pytest.fixture(autouse=True)
+def _float64_default():
+    """Every tensor these checks create without a dtype is float64; the
+    process-wide default is restored afterwards for the other test files."""
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(old)
 
 
 def _inputs(B=2, N=17, H=3, D=5, DV=4, G=6, wmode="hgd", bias=True, seed=0):
