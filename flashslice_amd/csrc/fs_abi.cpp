@@ -59,12 +59,25 @@ Geo geo_n(const fs_slice_params* p, int64_t target_blocks) {
   return g;
 }
 
+// partials per (b, h) of a whole-G launch: one per block of four waves
+int pb(const Geo& g) { return g.P / fs::kWavesPerBlock; }
+
 Geo geo_g(const fs_slice_params* p) {
   const int64_t nsg = (p->G + 31) / 32;
   return geo_n(p, (512 + nsg - 1) / nsg);
 }
 
-int64_t fused_target(int32_t op) { return op == FS_OP_DESLICE_FWD ? 1024 : 512; }
+// Blocks per launch of the whole-G kernels (measured on MI355X at N = 1e6,
+// H = 8, D = DV = G = 32): the kernels that write point rows run best with
+// about three times more blocks than stay resident (two waves per SIMD), so
+// that the hardware keeps refilling CUs as blocks finish.
+int64_t fused_target(int32_t op) {
+  switch (op) {
+    case FS_OP_DESLICE_FWD: return 1536;
+    case FS_OP_SLICE_BWD: return 1536;
+    default: return 512;
+  }
+}
 
 // ------------------------------------------------------------------ checks
 int32_t check_params(const fs_slice_params* p, const char* who) {
@@ -215,8 +228,9 @@ Workspace plan_ws(int32_t op, const fs_slice_params* p, char* base) {
   const int64_t bh = p->B * p->H;
   if (op == FS_OP_DESLICE_FWD || op == FS_OP_STATS) return w;
   if (family_of(p) == 1) {
+    // whole-G kernels leave one partial per block (its four waves summed)
     const Geo g = geo_n(p, fused_target(op));
-    w.part = take((size_t)(bh * g.P * wave_floats(op, p)));
+    w.part = take((size_t)(bh * pb(g) * wave_floats(op, p)));
   } else {
     const Geo gn = geo_n(p, 512), gg = geo_g(p);
     w.stats = take((size_t)(bh * 2 * p->N));
@@ -349,9 +363,11 @@ int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     rc = hip_check(fs::launch_blocked(fs::BK_SLICE_G, a, x->dtype, mode, st), who);
   }
   if (rc) return rc;
+  // partials: one per block (whole-G) or per wave (G-blocked)
+  const int np = family_of(p) == 1 ? pb(g) : g.P;
   fs::ReduceSegments rs{};
-  rs.seg[0] = seg(ws.part, wf, 0, g.P, G * DV, (int)p->B, (int)p->H, z_num);
-  rs.seg[1] = seg(ws.part, wf, (int64_t)G * DV, g.P, G, (int)p->B, (int)p->H, s);
+  rs.seg[0] = seg(ws.part, wf, 0, np, G * DV, (int)p->B, (int)p->H, z_num);
+  rs.seg[1] = seg(ws.part, wf, (int64_t)G * DV, np, G, (int)p->B, (int)p->H, s);
   rs.n = 2;
   return hip_check(fs::launch_reduce((int)p->B, (int)p->H, rs, st), who);
 }
@@ -439,9 +455,9 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     a.part = ws.part;
     rc = hip_check(fs::launch_fused_slice_bwd(a, x->dtype, mode, st), who);
     if (rc) return rc;
-    rs.seg[0] = seg(ws.part, wf, 0, g.P, G * D, Bw, Hw, dweight);
-    rs.seg[1] = seg(ws.part, wf, (int64_t)G * D, g.P, G, Bb, Hb, dbias);
-    rs.seg[2] = seg(ws.part, wf, (int64_t)G * D + G, g.P, 1, 1, (int)p->H, dtau);
+    rs.seg[0] = seg(ws.part, wf, 0, pb(g), G * D, Bw, Hw, dweight);
+    rs.seg[1] = seg(ws.part, wf, (int64_t)G * D, pb(g), G, Bb, Hb, dbias);
+    rs.seg[2] = seg(ws.part, wf, (int64_t)G * D + G, pb(g), 1, 1, (int)p->H, dtau);
   } else {
     const float* stats = stats_in;
     if (!stats) {
@@ -520,10 +536,10 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
     a.part = ws.part;
     rc = hip_check(fs::launch_fused_deslice_bwd(a, x->dtype, mode, st), who);
     if (rc) return rc;
-    rs.seg[0] = seg(ws.part, wf, 0, g.P, G * DV, (int)p->B, (int)p->H, dtokens);
-    rs.seg[1] = seg(ws.part, wf, offW, g.P, G * D, Bw, Hw, dweight);
-    rs.seg[2] = seg(ws.part, wf, offB, g.P, G, Bb, Hb, dbias);
-    rs.seg[3] = seg(ws.part, wf, offB + G, g.P, 1, 1, (int)p->H, dtau);
+    rs.seg[0] = seg(ws.part, wf, 0, pb(g), G * DV, (int)p->B, (int)p->H, dtokens);
+    rs.seg[1] = seg(ws.part, wf, offW, pb(g), G * D, Bw, Hw, dweight);
+    rs.seg[2] = seg(ws.part, wf, offB, pb(g), G, Bb, Hb, dbias);
+    rs.seg[3] = seg(ws.part, wf, offB + G, pb(g), 1, 1, (int)p->H, dtau);
   } else {
     const float* stats = stats_in;
     if (!stats) {

@@ -11,8 +11,9 @@
 // Every dot runs on the bf16 matrix cores (fs_mma.h): the ieee / tf32 /
 // tf32x3 levels as the exact three-piece split (MMA_X6, fp32-accurate), the
 // bf16 levels as plain bf16 MFMAs. Slot-indexed sums (z_num, s, dtokens, dW,
-// db, dtau) are accumulated per wave and written as per-wave partials that
-// fs_reduce.hip sums in a fixed order. The next tile's point rows are loaded
+// db, dtau) are accumulated per wave, summed over the block's four waves in
+// a fixed order, and written as per-block partials that fs_reduce.hip sums
+// in a fixed order. The next tile's point rows are loaded
 // while the current tile is computed.
 //
 // Reference kernels these replace: _slice_fwd_kernel (slice_ops.py:554-599),
@@ -73,6 +74,23 @@ __device__ __forceinline__ void build_frags(u32x4* dst, int n, int wid, int lane
     lds_put<M>(dst + i * frag_words<M>(), q, lane);
   }
 }
+
+// Sum the four waves' partials of a block in a fixed order (wave 0, 1, 2,
+// 3) through the LDS buffer `buf` (region 0: the loops' transpose tiles,
+// free once every wave has left its loop) and write the block's partial
+// (E floats) to `dst`. `put(buf, first)` stores (first wave) or adds this
+// wave's values; every element is owned by exactly one lane of each wave.
+template <typename Put>
+__device__ __forceinline__ void block_partial(float* buf, int E, int wid, float* dst, Put&& put) {
+  __syncthreads();
+  for (int w = 0; w < kWavesPerBlock; ++w) {
+    if (wid == w) put(buf, w == 0);
+    __syncthreads();
+  }
+  for (int i = threadIdx.x; i < E; i += 256) dst[i] = buf[i];
+  __syncthreads();
+}
+__device__ __forceinline__ void acc_put(float& t, float v, bool first) { t = first ? v : t + v; }
 
 // Block prologue shared by the four kernels: head constants, LDS carve-up,
 // the fp32 staging of W and tokens / dz_num, and the logits operand W
@@ -234,22 +252,27 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_fwd(Args a) {
     FS_TILE_LOOP(load, body, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
   };
   if (fast) run(std::true_type()); else run(std::false_type());
-  float* pw = a.part + ((int64_t)bh * a.P + pid) * part_floats_slice_fwd(G, DV);
+  float ssum[NGB];
 #pragma unroll
-  for (int gb = 0; gb < NGB; ++gb) {
-    const int g = 32 * gb + c;
-    const float s = pair_sum(sacc[gb]);
-    if (g < G) {
+  for (int gb = 0; gb < NGB; ++gb) ssum[gb] = pair_sum(sacc[gb]);
+  const int64_t E = part_floats_slice_fwd(G, DV);
+  float* pw = a.part + ((int64_t)bh * gridDim.x + blockIdx.x) * E;
+  block_partial(smem, (int)E, wid, pw, [&](float* buf, bool first) {
 #pragma unroll
-      for (int vb = 0; vb < NVB; ++vb)
+    for (int gb = 0; gb < NGB; ++gb) {
+      const int g = 32 * gb + c;
+      if (g < G) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int v = 32 * vb + kmap(r, h);
-          if (v < DV) pw[(int64_t)g * DV + v] = zacc[gb][vb][r];
-        }
-      if (h == 0) pw[(int64_t)G * DV + g] = s;
+        for (int vb = 0; vb < NVB; ++vb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int v = 32 * vb + kmap(r, h);
+            if (v < DV) acc_put(buf[g * DV + v], zacc[gb][vb][r], first);
+          }
+        if (h == 0) acc_put(buf[G * DV + g], ssum[gb], first);
+      }
     }
-  }
+  });
 }
 
 // ---------------------------------------------------------------- deslice fwd
@@ -311,9 +334,10 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_fwd(Args a) {
   if (fast) run(std::true_type()); else run(std::false_type());
 }
 
-// dx = ab W and dW += ab^T x, db += sum_n ab for the two backward kernels:
-// `om` holds ab = Lb / tau ([point-outer, slot-inner]); qWc the ready
-// fragments of W as [d-outer, g-inner] (index db * NGB + gb).
+// dx = Lb (W / tau) and dW += Lb^T x, db += sum_n Lb (scaled by 1 / tau
+// when the partials are written) for the two backward kernels: `om` holds
+// Lb ([point-outer, slot-inner]); qWc the ready fragments of W / tau as
+// [d-outer, g-inner] (index db * NGB + gb).
 #define FS_DX_DW(OM, QWC)                                                           \
   {                                                                                 \
     f32x16 o_[NDB];                                                                 \
@@ -368,6 +392,8 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
   });
   build_frags<MV>(qWc, NDB * NGB, wid, lane, [&](int i, float(&f)[16]) {
     lds_frag_colouter(f, sW, SM::SW, 32 * (i % NGB), 32 * (i / NGB), c, h);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) f[j] *= inv_tau;
   });
   for (int i = threadIdx.x; i < SM::GP; i += 256) sDS[i] = i < G ? a.ds[(int64_t)bh * G + i] : 0.f;
   FS_PROLOGUE_END
@@ -455,31 +481,36 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
         }
       }
       load_f(t + a.P);
-      dtacc += jacobian_tile<NGB>(om, w, t2, m2, inv_tau, pv, h);
+      dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
       FS_DX_DW(om, qWc)
     };
     load_f(pid);
     FS_TILE_LOOP(load, body, xA, xB)
   };
   if (fast) run(std::true_type()); else run(std::false_type());
-  float* pw = a.part + ((int64_t)bh * a.P + pid) * part_floats_slice_bwd(G, D);
+  float dbs[NGB];
 #pragma unroll
-  for (int gb = 0; gb < NGB; ++gb) {
-    const int g = 32 * gb + c;
-    const float s = pair_sum(dbacc[gb]);
-    if (g < G) {
+  for (int gb = 0; gb < NGB; ++gb) dbs[gb] = pair_sum(dbacc[gb]) * inv_tau;
+  const float dt = -kLn2 * inv_tau * half_wave_sum(dtacc);
+  const int64_t E = part_floats_slice_bwd(G, D);
+  float* pw = a.part + ((int64_t)bh * gridDim.x + blockIdx.x) * E;
+  block_partial(smem, (int)E, wid, pw, [&](float* buf, bool first) {
 #pragma unroll
-      for (int db = 0; db < NDB; ++db)
+    for (int gb = 0; gb < NGB; ++gb) {
+      const int g = 32 * gb + c;
+      if (g < G) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int d = 32 * db + kmap(r, h);
-          if (d < D) pw[(int64_t)g * D + d] = dW[gb][db][r];
-        }
-      if (h == 0) pw[(int64_t)G * D + g] = s;
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int d = 32 * db + kmap(r, h);
+            if (d < D) acc_put(buf[g * D + d], dW[gb][db][r] * inv_tau, first);
+          }
+        if (h == 0) acc_put(buf[G * D + g], dbs[gb], first);
+      }
     }
-  }
-  const float dt = half_wave_sum(dtacc);
-  if (lane == 0) pw[(int64_t)G * D + G] = -kLn2 * inv_tau * dt;
+    if (lane == 0) acc_put(buf[G * D + G], dt, first);
+  });
 }
 
 // ---------------------------------------------------------------- deslice bwd
@@ -495,6 +526,8 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_bwd(Args a) {
   });
   build_frags<MV>(qWc, NDB * NGB, wid, lane, [&](int i, float(&f)[16]) {
     lds_frag_colouter(f, sW, SM::SW, 32 * (i % NGB), 32 * (i / NGB), c, h);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) f[j] *= inv_tau;
   });
   FS_PROLOGUE_END
   f32x16 dT[NGB][NVB], dW[NGB][NDB];
@@ -576,39 +609,52 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_bwd(Args a) {
         }
       }
       load_g(t + a.P);
-      dtacc += jacobian_tile<NGB>(om, w, t2, m2, inv_tau, pv, h);
+      dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
       FS_DX_DW(om, qWc)
     };
     load_g(pid);
     FS_TILE_LOOP(load, body, xA, xB)
   };
   if (fast) run(std::true_type()); else run(std::false_type());
-  float* pw = a.part + ((int64_t)bh * a.P + pid) * part_floats_deslice_bwd(G, D, DV);
-  const int64_t offW = (int64_t)G * DV, offB = offW + (int64_t)G * D;
+  float dbs[NGB];
 #pragma unroll
-  for (int gb = 0; gb < NGB; ++gb) {
-    const int g = 32 * gb + c;
-    const float s = pair_sum(dbacc[gb]);
-    if (g < G) {
+  for (int gb = 0; gb < NGB; ++gb) dbs[gb] = pair_sum(dbacc[gb]) * inv_tau;
+  const float dt = -kLn2 * inv_tau * half_wave_sum(dtacc);
+  const int64_t offW = (int64_t)G * DV, E = part_floats_deslice_bwd(G, D, DV);
+  float* pw = a.part + ((int64_t)bh * gridDim.x + blockIdx.x) * E;
+  // two passes through the LDS buffer: dtokens, then dW, db, dtau
+  block_partial(smem, (int)offW, wid, pw, [&](float* buf, bool first) {
 #pragma unroll
-      for (int vb = 0; vb < NVB; ++vb)
+    for (int gb = 0; gb < NGB; ++gb) {
+      const int g = 32 * gb + c;
+      if (g < G) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int v = 32 * vb + kmap(r, h);
-          if (v < DV) pw[(int64_t)g * DV + v] = dT[gb][vb][r];
-        }
+        for (int vb = 0; vb < NVB; ++vb)
 #pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int d = 32 * db + kmap(r, h);
-          if (d < D) pw[offW + (int64_t)g * D + d] = dW[gb][db][r];
-        }
-      if (h == 0) pw[offB + g] = s;
+          for (int r = 0; r < 16; ++r) {
+            const int v = 32 * vb + kmap(r, h);
+            if (v < DV) acc_put(buf[g * DV + v], dT[gb][vb][r], first);
+          }
+      }
     }
-  }
-  const float dt = half_wave_sum(dtacc);
-  if (lane == 0) pw[offB + G] = -kLn2 * inv_tau * dt;
+  });
+  block_partial(smem, (int)(E - offW), wid, pw + offW, [&](float* buf, bool first) {
+#pragma unroll
+    for (int gb = 0; gb < NGB; ++gb) {
+      const int g = 32 * gb + c;
+      if (g < G) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int d = 32 * db + kmap(r, h);
+            if (d < D) acc_put(buf[g * D + d], dW[gb][db][r] * inv_tau, first);
+          }
+        if (h == 0) acc_put(buf[G * D + g], dbs[gb], first);
+      }
+    }
+    if (lane == 0) acc_put(buf[G * D + G], dt, first);
+  });
 }
 
 // ------------------------------------------------------------ launch templates

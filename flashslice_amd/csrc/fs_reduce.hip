@@ -1,13 +1,15 @@
 // Deterministic second level of every cross-tile reduction.
 //
-// The point-streaming kernels leave one partial per wave (a static
-// tile -> wave assignment). One launch per op sums them into every output
+// The point-streaming kernels leave one partial per wave (G-blocked family)
+// or per block of four waves (whole-G family), from a static tile -> wave
+// assignment. One launch per op sums them into every output
 // of the op (z_num and s; dW, db and dtau; ...), folding the batch / head
 // axes a parameter is shared along. Each block owns 32 consecutive output
 // elements of one segment; its 8 thread groups each sum a fixed,
-// interleaved subset of the contributing partials in fp64, and the 8 group
-// sums are added in a fixed order -- so repeated runs are bitwise identical
-// (no atomics). Reads are coalesced (32 consecutive floats per partial).
+// interleaved subset of the contributing partials in fp64 (four
+// accumulators, four loads in flight), and the group sums are added in a
+// fixed order -- so repeated runs are bitwise identical (no atomics). Reads
+// are coalesced (32 consecutive floats per partial).
 //
 // Replaces the reference's torch ``.sum`` over per-program partials
 // (slice_ops.py:481-500, 819, 843, 884-885; blocked.py:1367, 1402-1403,
@@ -39,24 +41,26 @@ __global__ __launch_bounds__(256) void k_reduce_segments(int B, int H, ReduceSeg
   const int nbs = sg.Bo > 1 ? 1 : B, nhs = sg.Ho > 1 ? 1 : H;
   const int b0 = sg.Bo > 1 ? ob : 0, h0 = sg.Ho > 1 ? oh : 0;
   const int C = nbs * nhs * P;  // contributors, ordered (b, h, p)
-  double acc0 = 0.0, acc1 = 0.0;
+  auto load = [&](int cc) -> double {
+    const int pp = cc % P, bhc = cc / P;
+    const int bb = b0 + bhc / nhs, hh = h0 + bhc % nhs;
+    return (double)part[((int64_t)(bb * H + hh) * P + pp) * wstride + sg.off + e];
+  };
+  // group grp sums contributors grp, grp + 8, ... into four accumulators
+  // (contributor grp + 8 j goes to accumulator j % 4), four loads in flight
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
   if (e < sg.E) {
-    int c = grp;
-    for (; c + 8 < C; c += 16) {
-      const int c1 = c + 8;
-      const int p0 = c % P, bh0 = c / P, p1 = c1 % P, bh1 = c1 / P;
-      const int b_0 = b0 + bh0 / nhs, h_0 = h0 + bh0 % nhs;
-      const int b_1 = b0 + bh1 / nhs, h_1 = h0 + bh1 % nhs;
-      acc0 += (double)part[((int64_t)(b_0 * H + h_0) * P + p0) * wstride + sg.off + e];
-      acc1 += (double)part[((int64_t)(b_1 * H + h_1) * P + p1) * wstride + sg.off + e];
+    int c = grp, j = 0;
+    for (; c + 24 < C; c += 32, j += 4) {
+      const double v0 = load(c), v1 = load(c + 8), v2 = load(c + 16), v3 = load(c + 24);
+      acc[0] += v0;
+      acc[1] += v1;
+      acc[2] += v2;
+      acc[3] += v3;
     }
-    if (c < C) {
-      const int p0 = c % P, bh0 = c / P;
-      const int b_0 = b0 + bh0 / nhs, h_0 = h0 + bh0 % nhs;
-      acc0 += (double)part[((int64_t)(b_0 * H + h_0) * P + p0) * wstride + sg.off + e];
-    }
+    for (; c < C; c += 8, ++j) acc[j & 3] += load(c);
   }
-  red[grp][el] = acc0 + acc1;
+  red[grp][el] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   __syncthreads();
   if (grp == 0 && e < sg.E) {
     double t = 0.0;

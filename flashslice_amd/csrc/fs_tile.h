@@ -36,12 +36,14 @@ __device__ __forceinline__ void logits_tile(float (&t2)[NGB][16], const float (&
 }
 
 // Softmax over the G slots of each point (lane pair c, c + 32 holds one
-// point). Returns w (zero for points beyond N), the row max m2 (log2 units)
-// and the row sum. The row sum is formed in a fixed order (lane-local, then
-// the partner), so both lanes of a pair hold the same value.
+// point). Shifts t2 in place to t2 - m2 (the exponent of each weight, which
+// the backward's temperature term reuses) and returns w (zero for points
+// beyond N), the row max m2 (log2 units) and the row sum. The row sum is
+// formed in a fixed order (lane-local, then the partner), so both lanes of a
+// pair hold the same value.
 template <int NGB>
 __device__ __forceinline__ void softmax_tile(float (&w)[NGB][16], float& m2, float& lsum,
-                                             const float (&t2)[NGB][16], bool pv) {
+                                             float (&t2)[NGB][16], bool pv) {
   float m = -INFINITY;
 #pragma unroll
   for (int gb = 0; gb < NGB; ++gb)
@@ -53,7 +55,8 @@ __device__ __forceinline__ void softmax_tile(float (&w)[NGB][16], float& m2, flo
   for (int gb = 0; gb < NGB; ++gb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float e = __builtin_amdgcn_exp2f(t2[gb][r] - m);
+      t2[gb][r] -= m;
+      const float e = __builtin_amdgcn_exp2f(t2[gb][r]);
       w[gb][r] = e;
       l += e;
     }
@@ -91,15 +94,15 @@ __device__ __forceinline__ void store_stats(float* stats, int bh, int N, int p, 
 
 // The softmax Jacobian of one tile given omega = dL/dw: Lb = w (omega -
 // delta), delta = sum_g w omega, both from the same rounded products.
-// Overwrites om with ab = Lb / tau and returns the row term
-// sum_g Lb (t2 - m2) of the temperature gradient (natural units up to a
-// factor ln 2; zero on lanes h = 1 and on points beyond N). Shifting the
-// logits by the row max is exact in real arithmetic (sum_g Lb = 0) and
-// keeps the terms small.
+// Overwrites om with Lb (the callers apply 1 / tau: to the W operand of dx
+// and to the dW, db partials) and returns the row term sum_g Lb (t2 - m2)
+// of the temperature gradient (natural units up to a factor ln 2; zero on
+// lanes h = 1 and on points beyond N). `t2s` holds t2 - m2 (softmax_tile's
+// shifted logits). Shifting the logits by the row max is exact in real
+// arithmetic (sum_g Lb = 0) and keeps the terms small.
 template <int NGB>
 __device__ __forceinline__ float jacobian_tile(float (&om)[NGB][16], const float (&w)[NGB][16],
-                                               const float (&t2)[NGB][16], float m2,
-                                               float inv_tau, bool pv, int h) {
+                                               const float (&t2s)[NGB][16], bool pv, int h) {
   float d = 0.f;
 #pragma unroll
   for (int gb = 0; gb < NGB; ++gb)
@@ -112,8 +115,8 @@ __device__ __forceinline__ float jacobian_tile(float (&om)[NGB][16], const float
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const float lb = w[gb][r] * (om[gb][r] - d);
-      rt = fmaf(lb, t2[gb][r] - m2, rt);
-      om[gb][r] = lb * inv_tau;
+      rt = fmaf(lb, t2s[gb][r], rt);
+      om[gb][r] = lb;
     }
   rt = pair_sum(rt);
   return (pv && h == 0) ? rt : 0.f;
