@@ -20,11 +20,14 @@ bench/parity_ops.py:148-151). Inputs follow BASELINE.json config 2: x, fx
 tau ~ U[0.3, 1.0]. ``value`` is points per second of the whole step.
 
 Printed: ONE JSON line with the driver's fields, plus ``roofline`` (the
-dominant kernel's algorithmic bytes per launch over its HIP-event time on
-its stream), ``step_roofline`` (all four ops' algorithmic bytes over the
-step), ``cpu_baseline`` (the CPU oracle -- the eager PyTorch softmax/einsum
-path -- timed on a bounded sample on this host's cores), ``peak_hbm_gb``,
-``per_op_ms`` and ``deterministic``.
+dominant op's algorithmic bytes per launch over its HIP-event time on its
+stream -- the op is its point kernel and the small fixed-order reduction of
+its partials; ``traffic`` is the HBM bytes rocprofv3 counted for it, from
+the committed profiles/<workload>_hbm_traffic.txt), ``step_roofline`` (all
+four ops' algorithmic bytes over the step), ``cpu_baseline`` (the CPU
+oracle -- the eager PyTorch softmax/einsum path -- timed on a bounded sample
+on this host's cores), ``peak_hbm_gb``, ``per_op_ms`` and
+``deterministic``.
 """
 
 import argparse
@@ -39,7 +42,6 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, published
-MFMA_F32_TFLOPS = 157.3         # MI355X dense fp32 MFMA, published
 EPS = 1e-5
 
 WORKLOADS = {
@@ -87,6 +89,30 @@ def alg_flops(B, N, H, D, DV, G):
             "slice_bwd": u * (3 * D + 2 * DV)}
 
 
+def measured_traffic(workload):
+    """HBM bytes per launch of each op's kernels as rocprofv3 counted them
+    (FETCH_SIZE + WRITE_SIZE, calibrated against a copy of known size), read
+    from the committed summary profiles/<workload>_hbm_traffic.txt (its
+    ``hbm_bytes_per_launch`` block); None where no summary exists."""
+    path = os.path.join(ROOT, "profiles", "%s_hbm_traffic.txt" % workload)
+    if not os.path.exists(path):
+        return None
+    out, on = {}, False
+    with open(path) as f:
+        for ln in f:
+            if ln.startswith("hbm_bytes_per_launch"):
+                on = True
+                continue
+            if on:
+                parts = ln.split()
+                if len(parts) != 2:
+                    if out:
+                        break
+                    continue
+                out[parts[0]] = int(float(parts[1]))
+    return out or None
+
+
 def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, ev=None):
     ops = torch.ops.flashslice
 
@@ -102,21 +128,21 @@ def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, ev=None):
     out = ops.flash_deslice(x, W, b, tau, tok, 0)
     mark(2)
     dx1, dtok, dW1, db1, dt1 = ops.flash_deslice_bwd(x, W, b, tau, tok, d_out, 0)
-    mark(3)
     dz = dzb + dtok / den
     ds = dsb - (dtok * tok).sum(-1) / den[..., 0]
+    mark(3)
     dx2, dfx, dW2, db2, dt2 = ops.flash_slice_bwd(x, fx, W, b, tau, dz, ds, 0)
     mark(4)
     return z, s, out, dx1, dtok, dW1, db1, dt1, dx2, dfx, dW2, db2, dt2
 
 
-def cpu_baseline(B, H, D, DV, G, layout, budget_s=20.0):
+def cpu_baseline(B, N, H, D, DV, G, layout, budget_s=20.0):
     """The eager PyTorch softmax/einsum path (the CPU oracle, fp32) on this
     host's cores, forward + backward of the same coupling on a bounded
     sample of points; returns points/s."""
     import oracle
     torch.set_num_threads(os.cpu_count() or 1)
-    n = 32768
+    n = min(32768, N)
     x, fx, W, b, tau, d_out, dzb, dsb = make_inputs(B, n, H, D, DV, G, layout, "cpu")
 
     def run():
@@ -128,9 +154,10 @@ def cpu_baseline(B, H, D, DV, G, layout, budget_s=20.0):
     t0 = time.perf_counter()
     run()
     one = time.perf_counter() - t0
-    # grow the sample until one run is ~1/4 of the budget, then time 3 runs
-    while one < budget_s / 8 and n < 1_000_000:
-        n *= 2
+    # grow the sample (up to the workload's N) until one run is ~1/8 of the
+    # budget, then time 3 runs
+    while one < budget_s / 8 and n < N:
+        n = min(2 * n, N)
         x, fx, W, b, tau, d_out, dzb, dsb = make_inputs(B, n, H, D, DV, G, layout, "cpu")
         t0 = time.perf_counter()
         run()
@@ -221,10 +248,11 @@ def main():
     total_bytes = sum(bytes_.values())
     total_flops = sum(flops.values())
     step_ach = total_bytes / (ms_step * 1e-3) / 1e9
+    traffic = measured_traffic(a.workload)
 
     cpu = None
     if not a.no_cpu_baseline:
-        v, n_s, thr = cpu_baseline(B, H, D, DV, G, layout)
+        v, n_s, thr = cpu_baseline(B, N, H, D, DV, G, layout)
         cpu = {"value": round(v / 1e6, 4), "unit": "Mpoints/s", "cores": thr, "kind": "port",
                "sample": "eager PyTorch softmax/einsum oracle (oracle/eager.py), fp32 fwd+bwd "
                          "of the same coupling on %d of the %d points, median of 3 runs, "
@@ -243,13 +271,14 @@ def main():
                    "weight": layout, "dot": "ieee"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": traffic.get(dom) if traffic else None,
+                     "traffic_source": ("profiles/%s_hbm_traffic.txt" % a.workload) if traffic
+                     else None,
                      "alg_bytes_per_launch": bytes_[dom], "ms_per_launch": round(per_op[dom], 4)},
         "step_roofline": {"alg_bytes": total_bytes, "achieved_GBs": round(step_ach, 1),
                           "hbm_frac": round(step_ach / HBM_PEAK_GBS, 4),
                           "alg_flops": total_flops,
-                          "mfma_f32_frac": round(total_flops / (ms_step * 1e-3) / 1e12
-                                                 / MFMA_F32_TFLOPS, 4)},
+                          "alg_tflops": round(total_flops / (ms_step * 1e-3) / 1e12, 2)},
         "per_op_ms": {k: round(v, 4) for k, v in per_op.items()},
         "peak_hbm_gb": round(peak_gb, 3),
         "nxhxg_gb": round(B * N * H * G * 4 / 1e9, 3),

@@ -438,28 +438,8 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
         for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xf[db]);
         FS_LOGITS(t2, xq)
       }
-      softmax_tile<NGB>(w, m2, lsum, t2, pv);
-      // dfx = w dz_num
-      {
-        f32x16 o[NVB];
-#pragma unroll
-        for (int vb = 0; vb < NVB; ++vb) o[vb] = zero16();
-#pragma unroll
-        for (int gb = 0; gb < NGB; ++gb) {
-          Frag<MV> wq;
-          prep<MV>(wq, w[gb]);
-#pragma unroll
-          for (int vb = 0; vb < NVB; ++vb) {
-            Frag<MV> zq;
-            lds_get<MV>(zq, qZc + (vb * NGB + gb) * FWV, lane);
-            o[vb] = mma<MV>(wq, zq, o[vb]);
-          }
-        }
-        const Rsrc rdf = rows_rsrc(df_b, df_sn, df_w, p0, N);
-#pragma unroll
-        for (int vb = 0; vb < NVB; ++vb) st_cols<T>(rdf, vcf[vb], (uint32_t)df_sn, o[vb]);
-      }
-      // omega = fx . dz_num + ds
+      // omega = fx . dz_num + ds (needs no weights: formed first, so that
+      // fx's buffer is reloaded for the next tile a whole tile ahead)
       float om[NGB][16];
       {
         Frag<MV> fq[NVB];
@@ -481,6 +461,27 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
         }
       }
       load_f(t + a.P);
+      softmax_tile<NGB>(w, m2, lsum, t2, pv);
+      // dfx = w dz_num
+      {
+        f32x16 o[NVB];
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) o[vb] = zero16();
+#pragma unroll
+        for (int gb = 0; gb < NGB; ++gb) {
+          Frag<MV> wq;
+          prep<MV>(wq, w[gb]);
+#pragma unroll
+          for (int vb = 0; vb < NVB; ++vb) {
+            Frag<MV> zq;
+            lds_get<MV>(zq, qZc + (vb * NGB + gb) * FWV, lane);
+            o[vb] = mma<MV>(wq, zq, o[vb]);
+          }
+        }
+        const Rsrc rdf = rows_rsrc(df_b, df_sn, df_w, p0, N);
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) st_cols<T>(rdf, vcf[vb], (uint32_t)df_sn, o[vb]);
+      }
       dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
       FS_DX_DW(om, qWc)
     };
@@ -570,27 +571,9 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_bwd(Args a) {
         for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xf[db]);
         FS_LOGITS(t2, xq)
       }
-      softmax_tile<NGB>(w, m2, lsum, t2, pv);
-      // dtokens += w^T d_out (rows of d_out beyond N read as zero)
-      {
-        Frag<MV> oTq[NVB];
-#pragma unroll
-        for (int vb = 0; vb < NVB; ++vb) {
-          float oT[16];
-          transpose32(oT, of[vb], lds, c, h);
-          prep<MV>(oTq[vb], oT);
-        }
-#pragma unroll
-        for (int gb = 0; gb < NGB; ++gb) {
-          float wT[16];
-          transpose32(wT, w[gb], lds, c, h);
-          Frag<MV> wTq;
-          prep<MV>(wTq, wT);
-#pragma unroll
-          for (int vb = 0; vb < NVB; ++vb) dT[gb][vb] = mma<MV>(oTq[vb], wTq, dT[gb][vb]);
-        }
-      }
-      // omega = d_out . tokens
+      // everything d_out feeds is prepared before the softmax (omega, and
+      // d_out transposed for dtokens), so that its buffer is reloaded for
+      // the next tile a whole tile ahead
       float om[NGB][16];
       {
         Frag<MV> oq[NVB];
@@ -608,7 +591,25 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_bwd(Args a) {
           from16(om[gb], o);
         }
       }
+      Frag<MV> oTq[NVB];
+#pragma unroll
+      for (int vb = 0; vb < NVB; ++vb) {
+        float oT[16];
+        transpose32(oT, of[vb], lds, c, h);
+        prep<MV>(oTq[vb], oT);
+      }
       load_g(t + a.P);
+      softmax_tile<NGB>(w, m2, lsum, t2, pv);
+      // dtokens += w^T d_out (rows of d_out beyond N read as zero)
+#pragma unroll
+      for (int gb = 0; gb < NGB; ++gb) {
+        float wT[16];
+        transpose32(wT, w[gb], lds, c, h);
+        Frag<MV> wTq;
+        prep<MV>(wTq, wT);
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) dT[gb][vb] = mma<MV>(oTq[vb], wTq, dT[gb][vb]);
+      }
       dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
       FS_DX_DW(om, qWc)
     };

@@ -25,6 +25,10 @@ typedef __amdgpu_buffer_rsrc_t Rsrc;
 constexpr int kRsrcWord3 = 0x00020000;
 // An offset beyond every resource built here (ranges are clamped below 2^31).
 constexpr uint32_t kOff = 0x80000000u;
+// Cache policy of the point streams: the default one. (Non-temporal loads
+// and stores -- each byte is touched once per kernel -- measured 20 %
+// slower on MI355X: the stores' 128-byte row segments are combined in L2.)
+constexpr int kStream = 0;
 
 // Rows [p0, N) of a slice with row stride snb bytes whose rows are rowb
 // bytes wide (the range ends with row N - 1, so rows >= N fall outside it
@@ -42,26 +46,26 @@ __device__ __forceinline__ Rsrc rows_rsrc(const void* base, int64_t snb, int64_t
 template <typename T> struct Buf;
 template <> struct Buf<float> {
   static __device__ __forceinline__ float ld1(Rsrc r, uint32_t off) {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kStream));
   }
   static __device__ __forceinline__ void ld4(float* o, Rsrc r, uint32_t off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kStream);
     o[0] = __uint_as_float(v[0]);
     o[1] = __uint_as_float(v[1]);
     o[2] = __uint_as_float(v[2]);
     o[3] = __uint_as_float(v[3]);
   }
   static __device__ __forceinline__ void st1(Rsrc r, uint32_t off, float v) {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, kStream);
   }
 };
 template <> struct Buf<__bf16> {
   static __device__ __forceinline__ float bits2f(uint32_t b16) { return __uint_as_float(b16 << 16); }
   static __device__ __forceinline__ float ld1(Rsrc r, uint32_t off) {
-    return bits2f(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+    return bits2f(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, kStream));
   }
   static __device__ __forceinline__ void ld4(float* o, Rsrc r, uint32_t off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kStream);
     o[0] = __uint_as_float(v[0] << 16);
     o[1] = __uint_as_float(v[0] & 0xffff0000u);
     o[2] = __uint_as_float(v[1] << 16);
@@ -69,7 +73,7 @@ template <> struct Buf<__bf16> {
   }
   static __device__ __forceinline__ void st1(Rsrc r, uint32_t off, float v) {
     const __bf16 b = (__bf16)v;
-    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, b), r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, b), r, off, 0, kStream);
   }
 };
 template <> struct Buf<_Float16> {
@@ -77,10 +81,10 @@ template <> struct Buf<_Float16> {
     return (float)__builtin_bit_cast(_Float16, (unsigned short)b16);
   }
   static __device__ __forceinline__ float ld1(Rsrc r, uint32_t off) {
-    return h2f(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+    return h2f(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, kStream));
   }
   static __device__ __forceinline__ void ld4(float* o, Rsrc r, uint32_t off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kStream);
     o[0] = h2f(v[0] & 0xffffu);
     o[1] = h2f(v[0] >> 16);
     o[2] = h2f(v[1] & 0xffffu);
@@ -88,7 +92,7 @@ template <> struct Buf<_Float16> {
   }
   static __device__ __forceinline__ void st1(Rsrc r, uint32_t off, float v) {
     const _Float16 b = (_Float16)v;
-    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, b), r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, b), r, off, 0, kStream);
   }
 };
 
