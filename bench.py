@@ -45,11 +45,12 @@ HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, published
 EPS = 1e-5
 
 WORKLOADS = {
-    # name: (B, N, H, D, DV, G, weight layout, description)
-    "c2": (1, 1_000_000, 8, 32, 32, 32, "hgd",
+    # name: (B, N, H, D, DV, G, weight layout, order, description)
+    "c2": (1, 1_000_000, 8, 32, 32, 32, "hgd", "slice-first",
            "C2: slice->deslice fwd+bwd, B=1 N=1e6 H=8 D=DV=32 G=32 fp32 ieee, per-head W"),
-    "c4": (4, 262_144, 8, 32, 64, 64, "bhgd",
-           "C4: B=4 N=262144 H=8 D=32 DV=64 G=64 fp32, per-sample W"),
+    "c4": (4, 262_144, 8, 32, 64, 64, "bhgd", "deslice-first",
+           "C4: deslice->slice fwd+bwd, B=4 N=262144 H=8 D=32 DV=64 G=64 fp32 ieee, "
+           "per-sample W, given tokens"),
 }
 
 
@@ -66,8 +67,9 @@ def make_inputs(B, N, H, D, DV, G, layout, device, seed=0):
     d_out = torch.randn(B, N, H, DV, generator=g)
     dzb = torch.randn(B, H, G, DV, generator=g)
     dsb = torch.randn(B, H, G, generator=g)
+    tok = torch.randn(B, H, G, DV, generator=g)
     to = lambda t: t.to(device)  # noqa: E731
-    return tuple(map(to, (x, fx, W, b, tau, d_out, dzb, dsb)))
+    return tuple(map(to, (x, fx, W, b, tau, d_out, dzb, dsb, tok)))
 
 
 def alg_bytes(B, N, H, D, DV, e=4):
@@ -77,7 +79,7 @@ def alg_bytes(B, N, H, D, DV, e=4):
     writes dx, dfx."""
     pts = B * N * H
     return {"slice_fwd": pts * (D + DV) * e, "deslice_fwd": pts * (D + DV) * e,
-            "deslice_bwd": pts * (D + 2 * DV) * e, "slice_bwd": pts * (2 * D + 2 * DV) * e}
+            "deslice_bwd": pts * (2 * D + DV) * e, "slice_bwd": pts * (2 * D + 2 * DV) * e}
 
 
 def alg_flops(B, N, H, D, DV, G):
@@ -113,41 +115,58 @@ def measured_traffic(workload):
     return out or None
 
 
-def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, ev=None):
+OPS = ("slice_fwd", "deslice_fwd", "deslice_bwd", "slice_bwd")
+
+
+def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", ev=None):
+    """One coupling step, forward and backward. slice-first: tokens come from
+    the slice (tokens = z / (s + eps)) and the upstream gradients reach z and
+    s through them too; deslice-first: the given tokens are deslided, then
+    the points are slided again (config 4's persistent point stream), and
+    the backward runs in autograd's order (slice, then deslice). ``ev``: a
+    (start, end) event pair per op name, recorded around exactly that op."""
     ops = torch.ops.flashslice
 
-    def mark(i):
-        if ev is not None:
-            ev[i].record()
+    def timed(name, fn, *args):
+        if ev is None:
+            return fn(*args)
+        ev[name][0].record()
+        r = fn(*args)
+        ev[name][1].record()
+        return r
 
-    mark(0)
-    z, s = ops.flash_slice(x, fx, W, b, tau, 0)
-    mark(1)
+    if order == "deslice-first":
+        out = timed("deslice_fwd", ops.flash_deslice, x, W, b, tau, tok0, 0)
+        z, s = timed("slice_fwd", ops.flash_slice, x, fx, W, b, tau, 0)
+        dx2, dfx, dW2, db2, dt2 = timed("slice_bwd", ops.flash_slice_bwd, x, fx, W, b, tau,
+                                        dzb, dsb, 0)
+        dx1, dtok, dW1, db1, dt1 = timed("deslice_bwd", ops.flash_deslice_bwd, x, W, b, tau,
+                                         tok0, d_out, 0)
+        return z, s, out, dx1, dtok, dW1, db1, dt1, dx2, dfx, dW2, db2, dt2
+    z, s = timed("slice_fwd", ops.flash_slice, x, fx, W, b, tau, 0)
     den = (s + EPS)[..., None]
     tok = z / den
-    out = ops.flash_deslice(x, W, b, tau, tok, 0)
-    mark(2)
-    dx1, dtok, dW1, db1, dt1 = ops.flash_deslice_bwd(x, W, b, tau, tok, d_out, 0)
+    out = timed("deslice_fwd", ops.flash_deslice, x, W, b, tau, tok, 0)
+    dx1, dtok, dW1, db1, dt1 = timed("deslice_bwd", ops.flash_deslice_bwd, x, W, b, tau, tok,
+                                     d_out, 0)
     dz = dzb + dtok / den
     ds = dsb - (dtok * tok).sum(-1) / den[..., 0]
-    mark(3)
-    dx2, dfx, dW2, db2, dt2 = ops.flash_slice_bwd(x, fx, W, b, tau, dz, ds, 0)
-    mark(4)
+    dx2, dfx, dW2, db2, dt2 = timed("slice_bwd", ops.flash_slice_bwd, x, fx, W, b, tau, dz, ds, 0)
     return z, s, out, dx1, dtok, dW1, db1, dt1, dx2, dfx, dW2, db2, dt2
 
 
-def cpu_baseline(B, N, H, D, DV, G, layout, budget_s=20.0):
+def cpu_baseline(B, N, H, D, DV, G, layout, order, budget_s=20.0):
     """The eager PyTorch softmax/einsum path (the CPU oracle, fp32) on this
     host's cores, forward + backward of the same coupling on a bounded
     sample of points; returns points/s."""
     import oracle
     torch.set_num_threads(os.cpu_count() or 1)
     n = min(32768, N)
-    x, fx, W, b, tau, d_out, dzb, dsb = make_inputs(B, n, H, D, DV, G, layout, "cpu")
+    x, fx, W, b, tau, d_out, dzb, dsb, tok = make_inputs(B, n, H, D, DV, G, layout, "cpu")
 
     def run():
-        leaves = [t.clone().requires_grad_(True) for t in (x, fx, W, b, tau)]
-        out, z, s = oracle.coupling(*leaves, order="slice-first")
+        leaves = [t.clone().requires_grad_(True) for t in (x, fx, W, b, tau, tok)]
+        out, z, s = oracle.coupling(*leaves[:5], tokens=leaves[5], order=order)
         oracle.coupling_loss(out, z, s, d_out, dzb, dsb).backward()
 
     run()
@@ -158,7 +177,7 @@ def cpu_baseline(B, N, H, D, DV, G, layout, budget_s=20.0):
     # budget, then time 3 runs
     while one < budget_s / 8 and n < N:
         n = min(2 * n, N)
-        x, fx, W, b, tau, d_out, dzb, dsb = make_inputs(B, n, H, D, DV, G, layout, "cpu")
+        x, fx, W, b, tau, d_out, dzb, dsb, tok = make_inputs(B, n, H, D, DV, G, layout, "cpu")
         t0 = time.perf_counter()
         run()
         one = time.perf_counter() - t0
@@ -193,7 +212,7 @@ def main():
     import flashslice_amd.kernels  # noqa: F401  -- registers torch.ops.flashslice
     from flashslice_amd.kernels import _hip
 
-    B, N, H, D, DV, G, layout, desc = WORKLOADS[a.workload]
+    B, N, H, D, DV, G, layout, order, desc = WORKLOADS[a.workload]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     inputs = make_inputs(B, N, H, D, DV, G, layout, dev)
@@ -210,12 +229,12 @@ def main():
         del probe
 
     for _ in range(a.warmup):
-        step_ops(*inputs)
+        step_ops(*inputs, order=order)
     torch.cuda.synchronize()
 
     # determinism: two steps bitwise equal
-    r1 = [t.clone() for t in step_ops(*inputs)]
-    r2 = step_ops(*inputs)
+    r1 = [t.clone() for t in step_ops(*inputs, order=order)]
+    r2 = step_ops(*inputs, order=order)
     deterministic = all(torch.equal(u, v) for u, v in zip(r1, r2))
     del r1, r2
 
@@ -223,24 +242,22 @@ def main():
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
     base = torch.cuda.memory_allocated()
-    res = step_ops(*inputs)
+    res = step_ops(*inputs, order=order)
     torch.cuda.synchronize()
     peak_gb = (torch.cuda.max_memory_allocated() - base) / 1e9
     del res
 
     # timed region: K steps, per-op HIP events on the launch stream
-    stream = torch.cuda.current_stream()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(a.steps)]
+    evs = [{n: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for n in OPS} for _ in range(a.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(a.steps):
-        step_ops(*inputs, ev=evs[i])
+        step_ops(*inputs, order=order, ev=evs[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = 1e3 * wall / a.steps
-    names = ("slice_fwd", "deslice_fwd", "deslice_bwd", "slice_bwd")
-    per_op = {n: sum(e[i].elapsed_time(e[i + 1]) for e in evs) / a.steps
-              for i, n in enumerate(names)}
+    per_op = {n: sum(e[n][0].elapsed_time(e[n][1]) for e in evs) / a.steps for n in OPS}
     bytes_ = alg_bytes(B, N, H, D, DV)
     flops = alg_flops(B, N, H, D, DV, G)
     dom = max(per_op, key=per_op.get)
@@ -252,7 +269,7 @@ def main():
 
     cpu = None
     if not a.no_cpu_baseline:
-        v, n_s, thr = cpu_baseline(B, N, H, D, DV, G, layout)
+        v, n_s, thr = cpu_baseline(B, N, H, D, DV, G, layout, order)
         cpu = {"value": round(v / 1e6, 4), "unit": "Mpoints/s", "cores": thr, "kind": "port",
                "sample": "eager PyTorch softmax/einsum oracle (oracle/eager.py), fp32 fwd+bwd "
                          "of the same coupling on %d of the %d points, median of 3 runs, "
@@ -268,7 +285,7 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
         "config": {"workload": desc, "B": B, "N": N, "H": H, "D": D, "DV": DV, "G": G,
-                   "weight": layout, "dot": "ieee"},
+                   "weight": layout, "order": order, "dot": "ieee"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
                      "traffic": traffic.get(dom) if traffic else None,

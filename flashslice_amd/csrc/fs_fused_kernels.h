@@ -188,9 +188,15 @@ __device__ __forceinline__ void acc_put(float& t, float v, bool first) { t = fir
   }
 #define FS_ARGS2(X, Y) X, Y
 
+// Waves per SIMD a whole-G kernel is compiled for: two (256 registers per
+// lane) for one block of 32 on every axis, one (512, the accumulators in
+// AGPRs) for the wider shapes, whose slot accumulators and operand fragments
+// spill at 256.
+constexpr int fused_waves(int ngb, int ndb, int nvb) { return ngb * ndb * nvb == 1 ? 2 : 1; }
+
 // ------------------------------------------------------------------ slice fwd
 template <typename T, int DK, int NGB, int NDB, int NVB>
-__global__ __launch_bounds__(256, 2) void k_fused_slice_fwd(Args a) {
+__global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice_fwd(Args a) {
   FS_PROLOGUE(NGB, NDB, NVB, 0)
   FS_PROLOGUE_END
   f32x16 zacc[NGB][NVB];
@@ -277,7 +283,7 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_fwd(Args a) {
 
 // ---------------------------------------------------------------- deslice fwd
 template <typename T, int DK, int NGB, int NDB, int NVB>
-__global__ __launch_bounds__(256, 2) void k_fused_deslice_fwd(Args a) {
+__global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_deslice_fwd(Args a) {
   FS_PROLOGUE(NGB, NDB, NVB, NVB * NGB)
   // tokens as [v-outer, g-inner]: qV[vb * NGB + gb]
   build_frags<MV>(qV, NVB * NGB, wid, lane, [&](int i, float(&f)[16]) {
@@ -377,7 +383,7 @@ __global__ __launch_bounds__(256, 2) void k_fused_deslice_fwd(Args a) {
 
 // ------------------------------------------------------------------ slice bwd
 template <typename T, int DK, int NGB, int NDB, int NVB>
-__global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
+__global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice_bwd(Args a) {
   FS_PROLOGUE(NGB, NDB, NVB, 2 * NGB * NVB + NDB * NGB)
   // dz_num as [g-outer, v-inner] (omega, qZr[gb * NVB + vb]) and [v-outer,
   // g-inner] (dfx, qZc[vb * NGB + gb]); W as [d-outer, g-inner] (dx).
@@ -516,7 +522,7 @@ __global__ __launch_bounds__(256, 2) void k_fused_slice_bwd(Args a) {
 
 // ---------------------------------------------------------------- deslice bwd
 template <typename T, int DK, int NGB, int NDB, int NVB>
-__global__ __launch_bounds__(256, 2) void k_fused_deslice_bwd(Args a) {
+__global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_deslice_bwd(Args a) {
   FS_PROLOGUE(NGB, NDB, NVB, NGB * NVB + NDB * NGB)
   // tokens as [g-outer, v-inner] (omega, qTr[gb * NVB + vb]); W as [d-outer,
   // g-inner] (dx).
