@@ -31,6 +31,7 @@ on this host's cores), ``peak_hbm_gb``, ``per_op_ms`` and
 """
 
 import argparse
+import functools
 import json
 import os
 import sys
@@ -42,16 +43,24 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, published
+MFMA_PEAK_TFLOPS = {"ieee": 157.3, "bf16": 2500.0}  # MI355X dense fp32 / bf16 MFMA, published
 EPS = 1e-5
 
 WORKLOADS = {
     # name: (B, N, H, D, DV, G, weight layout, order, description)
+    # C2 is bounded by HBM; C3 and C4 by the matrix cores
     "c2": (1, 1_000_000, 8, 32, 32, 32, "hgd", "slice-first",
            "C2: slice->deslice fwd+bwd, B=1 N=1e6 H=8 D=DV=32 G=32 fp32 ieee, per-head W"),
+    "c3-256": (1, 1_000_000, 8, 32, 32, 256, "hgd", "slice-first",
+               "C3: slice->deslice fwd+bwd, B=1 N=1e6 H=8 D=DV=32 G=256 fp32 ieee, per-head W"),
+    "c3-1024": (1, 1_000_000, 8, 32, 32, 1024, "hgd", "slice-first",
+                "C3: slice->deslice fwd+bwd, B=1 N=1e6 H=8 D=DV=32 G=1024 fp32 ieee, per-head W"),
     "c4": (4, 262_144, 8, 32, 64, 64, "bhgd", "deslice-first",
            "C4: deslice->slice fwd+bwd, B=4 N=262144 H=8 D=32 DV=64 G=64 fp32 ieee, "
            "per-sample W, given tokens"),
 }
+# dot level per run (reference slice_ops.py:336-343): 0 ieee; 3 bf16 (bf16 inputs)
+DOTS = {"ieee": 0, "bf16": 3}
 
 
 def make_inputs(B, N, H, D, DV, G, layout, device, seed=0):
@@ -118,13 +127,18 @@ def measured_traffic(workload):
 OPS = ("slice_fwd", "deslice_fwd", "deslice_bwd", "slice_bwd")
 
 
-def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", ev=None):
-    """One coupling step, forward and backward. slice-first: tokens come from
-    the slice (tokens = z / (s + eps)) and the upstream gradients reach z and
-    s through them too; deslice-first: the given tokens are deslided, then
-    the points are slided again (config 4's persistent point stream), and
-    the backward runs in autograd's order (slice, then deslice). ``ev``: a
-    (start, end) event pair per op name, recorded around exactly that op."""
+def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", dot=0,
+             blocked=False, ev=None):
+    """One coupling step, forward and backward, through the operators the
+    public API routes the shape to (reference slice_ops.py:961-1022): the
+    single-tile ops, or (``blocked``) the blocked ops, which carry the
+    forward's softmax statistics into the other pass and the backward.
+    slice-first: tokens come from the slice (tokens = z / (s + eps)) and the
+    upstream gradients reach z and s through them too; deslice-first: the
+    given tokens are deslided, then the points are slided again (config 4's
+    persistent point stream), and the backward runs in autograd's order
+    (slice, then deslice). ``ev``: a (start, end) event pair per op name,
+    recorded around exactly that op."""
     ops = torch.ops.flashslice
 
     def timed(name, fn, *args):
@@ -135,23 +149,31 @@ def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", ev=No
         ev[name][1].record()
         return r
 
+    if blocked:
+        slice_f = lambda st: ops.slice_blk(x, fx, W, b, tau, st, dot)  # noqa: E731
+        deslice_f = lambda tk, st: ops.deslice_blk(x, W, b, tau, tk, st, dot)  # noqa: E731
+        slice_b = lambda st, dz, ds: ops.slice_blk_bwd(x, fx, W, b, tau, st, dz, ds, dot)  # noqa
+        deslice_b = lambda tk, st: ops.deslice_blk_bwd(x, W, b, tau, tk, st, d_out, dot)  # noqa
+    else:
+        slice_f = lambda st: ops.flash_slice(x, fx, W, b, tau, dot) + (None,)  # noqa: E731
+        deslice_f = lambda tk, st: (ops.flash_deslice(x, W, b, tau, tk, dot), None)  # noqa
+        slice_b = lambda st, dz, ds: ops.flash_slice_bwd(x, fx, W, b, tau, dz, ds, dot)  # noqa
+        deslice_b = lambda tk, st: ops.flash_deslice_bwd(x, W, b, tau, tk, d_out, dot)  # noqa
+
     if order == "deslice-first":
-        out = timed("deslice_fwd", ops.flash_deslice, x, W, b, tau, tok0, 0)
-        z, s = timed("slice_fwd", ops.flash_slice, x, fx, W, b, tau, 0)
-        dx2, dfx, dW2, db2, dt2 = timed("slice_bwd", ops.flash_slice_bwd, x, fx, W, b, tau,
-                                        dzb, dsb, 0)
-        dx1, dtok, dW1, db1, dt1 = timed("deslice_bwd", ops.flash_deslice_bwd, x, W, b, tau,
-                                         tok0, d_out, 0)
+        out, st = timed("deslice_fwd", deslice_f, tok0, None)
+        z, s, _ = timed("slice_fwd", slice_f, st)
+        dx2, dfx, dW2, db2, dt2 = timed("slice_bwd", slice_b, st, dzb, dsb)
+        dx1, dtok, dW1, db1, dt1 = timed("deslice_bwd", deslice_b, tok0, st)
         return z, s, out, dx1, dtok, dW1, db1, dt1, dx2, dfx, dW2, db2, dt2
-    z, s = timed("slice_fwd", ops.flash_slice, x, fx, W, b, tau, 0)
+    z, s, st = timed("slice_fwd", slice_f, None)
     den = (s + EPS)[..., None]
     tok = z / den
-    out = timed("deslice_fwd", ops.flash_deslice, x, W, b, tau, tok, 0)
-    dx1, dtok, dW1, db1, dt1 = timed("deslice_bwd", ops.flash_deslice_bwd, x, W, b, tau, tok,
-                                     d_out, 0)
+    out, _ = timed("deslice_fwd", deslice_f, tok, st)
+    dx1, dtok, dW1, db1, dt1 = timed("deslice_bwd", deslice_b, tok, st)
     dz = dzb + dtok / den
     ds = dsb - (dtok * tok).sum(-1) / den[..., 0]
-    dx2, dfx, dW2, db2, dt2 = timed("slice_bwd", ops.flash_slice_bwd, x, fx, W, b, tau, dz, ds, 0)
+    dx2, dfx, dW2, db2, dt2 = timed("slice_bwd", slice_b, st, dz, ds)
     return z, s, out, dx1, dtok, dW1, db1, dt1, dx2, dfx, dW2, db2, dt2
 
 
@@ -196,6 +218,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--dot", default="ieee", choices=sorted(DOTS),
+                    help="dot level: ieee (fp32 inputs) or bf16 (x_mid, fx_mid, W in bf16)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="before the warmup, copy x once (B*N*H*D*4 bytes read and written): "
@@ -215,7 +239,14 @@ def main():
     B, N, H, D, DV, G, layout, order, desc = WORKLOADS[a.workload]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    inputs = make_inputs(B, N, H, D, DV, G, layout, dev)
+    inputs = list(make_inputs(B, N, H, D, DV, G, layout, dev))
+    dot = DOTS[a.dot]
+    if a.dot == "bf16":  # reference bench/parity_ops.py:134-136: activations and W in bf16
+        for i in (0, 1, 2, 3, 5):
+            inputs[i] = inputs[i].bfloat16()
+    from flashslice_amd.kernels.slice_ops import _use_blocked
+    blocked = _use_blocked(D, G, DV, dot)
+    run_step = functools.partial(step_ops, *inputs, order=order, dot=dot, blocked=blocked)
     torch.cuda.synchronize()
     print("[bench] %s; library %s" % (desc, _hip.lib().fs_version().decode()),
           file=sys.stderr, flush=True)
@@ -224,17 +255,18 @@ def main():
         probe = torch.empty_like(inputs[0])
         probe.copy_(inputs[0])
         torch.cuda.synchronize()
-        print("[bench] copy probe: %d bytes read, %d written" % (
-            probe.numel() * 4, probe.numel() * 4), file=sys.stderr, flush=True)
+        nb = probe.numel() * probe.element_size()
+        print("[bench] copy probe: %d bytes read, %d written" % (nb, nb), file=sys.stderr,
+              flush=True)
         del probe
 
     for _ in range(a.warmup):
-        step_ops(*inputs, order=order)
+        run_step()
     torch.cuda.synchronize()
 
     # determinism: two steps bitwise equal
-    r1 = [t.clone() for t in step_ops(*inputs, order=order)]
-    r2 = step_ops(*inputs, order=order)
+    r1 = [t.clone() for t in run_step()]
+    r2 = run_step()
     deterministic = all(torch.equal(u, v) for u, v in zip(r1, r2))
     del r1, r2
 
@@ -242,7 +274,7 @@ def main():
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
     base = torch.cuda.memory_allocated()
-    res = step_ops(*inputs, order=order)
+    res = run_step()
     torch.cuda.synchronize()
     peak_gb = (torch.cuda.max_memory_allocated() - base) / 1e9
     del res
@@ -253,15 +285,16 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(a.steps):
-        step_ops(*inputs, order=order, ev=evs[i])
+        run_step(ev=evs[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = 1e3 * wall / a.steps
     per_op = {n: sum(e[n][0].elapsed_time(e[n][1]) for e in evs) / a.steps for n in OPS}
-    bytes_ = alg_bytes(B, N, H, D, DV)
+    bytes_ = alg_bytes(B, N, H, D, DV, 2 if a.dot == "bf16" else 4)
     flops = alg_flops(B, N, H, D, DV, G)
     dom = max(per_op, key=per_op.get)
     ach = bytes_[dom] / (per_op[dom] * 1e-3) / 1e9
+    ach_tf = flops[dom] / (per_op[dom] * 1e-3) / 1e12
     total_bytes = sum(bytes_.values())
     total_flops = sum(flops.values())
     step_ach = total_bytes / (ms_step * 1e-3) / 1e9
@@ -283,15 +316,17 @@ def main():
         "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f32", "data": "synthetic",
+        "dtype": "f32" if a.dot == "ieee" else "bf16", "data": "synthetic",
         "config": {"workload": desc, "B": B, "N": N, "H": H, "D": D, "DV": DV, "G": G,
-                   "weight": layout, "order": order, "dot": "ieee"},
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                     "traffic": traffic.get(dom) if traffic else None,
-                     "traffic_source": ("profiles/%s_hbm_traffic.txt" % a.workload) if traffic
-                     else None,
-                     "alg_bytes_per_launch": bytes_[dom], "ms_per_launch": round(per_op[dom], 4)},
+                   "weight": layout, "order": order, "dot": a.dot,
+                   "ops": "blocked" if blocked else "single-tile"},
+        "roofline": ({"bound": "hbm", "kernel": dom, "achieved": round(ach, 1),
+                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4)}
+                     if a.workload == "c2" else
+                     {"bound": "mfma", "kernel": dom, "achieved": round(ach_tf, 2),
+                      "peak": MFMA_PEAK_TFLOPS[a.dot], "unit": "TFLOP/s",
+                      "frac": round(ach_tf / MFMA_PEAK_TFLOPS[a.dot], 4)}),
+        "traffic_source": ("profiles/%s_hbm_traffic.txt" % a.workload) if traffic else None,
         "step_roofline": {"alg_bytes": total_bytes, "achieved_GBs": round(step_ach, 1),
                           "hbm_frac": round(step_ach / HBM_PEAK_GBS, 4),
                           "alg_flops": total_flops,
@@ -302,6 +337,10 @@ def main():
         "deterministic": deterministic,
         "cpu_baseline": cpu,
     }
+    line["roofline"].update({
+        "traffic": traffic.get(dom) if traffic else None,
+        "alg_bytes_per_launch": bytes_[dom], "alg_flops_per_launch": flops[dom],
+        "ms_per_launch": round(per_op[dom], 4)})
     print(json.dumps(line), flush=True)
 
 

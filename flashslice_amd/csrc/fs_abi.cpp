@@ -212,8 +212,12 @@ struct Workspace {
   float* lsum = nullptr;   // (B, H, N)
   float* part2 = nullptr;  // (B H, P_n)
   float* part = nullptr;   // (B H, P, wave_floats)
+  float* frags = nullptr;  // prepared operand fragments (G-blocked, widths <= 64)
   size_t bytes = 0;
 };
+
+// G-blocked calls served by the prepared-fragment kernels
+bool gp_on(const fs_slice_params* p) { return fs::gp_serves((int)p->D, (int)p->DV); }
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
@@ -226,7 +230,16 @@ Workspace plan_ws(int32_t op, const fs_slice_params* p, char* base) {
     return ptr;
   };
   const int64_t bh = p->B * p->H;
-  if (op == FS_OP_DESLICE_FWD || op == FS_OP_STATS) return w;
+  // the fragment buffer: sized for the largest (fp32-accurate) fragments,
+  // whatever the call's dtype
+  const bool blocked = op == FS_OP_STATS || family_of(p) == 2;
+  if (blocked && gp_on(p))
+    w.frags = take((size_t)fs::gp_layout((int)p->B, (int)p->H, (int)p->G, (int)p->D, (int)p->DV,
+                                         0).total_u32x4 * 4);
+  if (op == FS_OP_DESLICE_FWD || op == FS_OP_STATS) {
+    w.bytes = off;
+    return w;
+  }
   if (family_of(p) == 1) {
     // whole-G kernels leave one partial per block (its four waves summed)
     const Geo g = geo_n(p, fused_target(op));
@@ -269,9 +282,22 @@ fs::ReduceSegment seg(const float* part, int64_t wstride, int64_t off, int P, in
   return s;
 }
 
-// statistics of the logits into `stats` with the point-owned stats kernel
+// Prepared operand fragments of one G-blocked call (k_gp_prep) into the
+// workspace, from a's W, bias, tau and (when set) tokens / dz_num and ds.
+int32_t gp_prepare(fs::Args& a, const fs_slice_params* p, const Workspace& ws, int mode,
+                   hipStream_t st, const char* who) {
+  if (!gp_on(p)) return FS_OK;
+  const fs::GpLayout l =
+      fs::gp_layout((int)p->B, (int)p->H, (int)p->G, (int)p->D, (int)p->DV, mode);
+  a.frags = ws.frags;
+  for (int k = 0; k < 6; ++k) a.foff[k] = l.off[k];
+  return hip_check(fs::launch_gp_prep(a, mode, st), who);
+}
+
+// statistics of the logits into `stats` with the point-owned stats kernel;
+// `prepared`: a call's Args whose fragments are already built
 int32_t run_stats(const fs_points* x, const fs_slice_params* p, float* stats, int two_pass,
-                  hipStream_t st, const char* who) {
+                  const fs::Args& prepared, hipStream_t st, const char* who) {
   const Geo g = geo_n(p, 512);
   fs::Args a = base_args(p, g);
   set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
@@ -279,6 +305,8 @@ int32_t run_stats(const fs_points* x, const fs_slice_params* p, float* stats, in
   a.fast = a.vec_x && full_widths(p);
   a.stats_out = stats;
   a.two_pass = two_pass;
+  a.frags = prepared.frags;
+  for (int k = 0; k < 6; ++k) a.foff[k] = prepared.foff[k];
   return hip_check(fs::launch_blocked(fs::BK_STATS, a, x->dtype, mode_of(p->dot, x->dtype), st),
                    who);
 }
@@ -303,13 +331,19 @@ size_t fs_workspace_bytes(int32_t op, const fs_slice_params* p) {
 
 int32_t fs_compute_stats(const fs_points* x, const fs_slice_params* p, float* stats,
                          int32_t two_pass, void* workspace, size_t workspace_bytes, void* stream) {
-  (void)workspace; (void)workspace_bytes;
   const char* who = "fs_compute_stats";
   int32_t rc = check_params(p, who);
   if (!rc) rc = check_points(x, "x_mid", p->D, who);
   if (rc) return rc;
   if (!stats) return fail(FS_ERR_INVALID, "%s: stats is NULL", who);
-  return run_stats(x, p, stats, two_pass ? 1 : 0, (hipStream_t)stream, who);
+  const Workspace ws = plan_ws(FS_OP_STATS, p, (char*)workspace);
+  rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  fs::Args a = base_args(p, geo_n(p, 512));
+  rc = gp_prepare(a, p, ws, mode_of(p->dot, x->dtype), st, who);
+  if (rc) return rc;
+  return run_stats(x, p, stats, two_pass ? 1 : 0, a, st, who);
 }
 
 int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_params* p,
@@ -344,13 +378,6 @@ int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     a.stats_out = stats_out;
     rc = hip_check(fs::launch_fused_slice_fwd(a, x->dtype, mode, st), who);
   } else {
-    const float* stats = stats_in;
-    if (!stats) {
-      float* dst = stats_out ? stats_out : ws.stats;
-      rc = run_stats(x, p, dst, 0, st, who);
-      if (rc) return rc;
-      stats = dst;
-    }
     g = geo_g(p);
     fs::Args a = base_args(p, g);
     set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
@@ -359,6 +386,15 @@ int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     a.vec_f = vec_ok(fx);
     a.fast = a.vec_x && a.vec_f && full_widths(p);
     a.part = ws.part;
+    rc = gp_prepare(a, p, ws, mode, st, who);
+    if (rc) return rc;
+    const float* stats = stats_in;
+    if (!stats) {
+      float* dst = stats_out ? stats_out : ws.stats;
+      rc = run_stats(x, p, dst, 0, a, st, who);
+      if (rc) return rc;
+      stats = dst;
+    }
     a.stats_in = stats;
     rc = hip_check(fs::launch_blocked(fs::BK_SLICE_G, a, x->dtype, mode, st), who);
   }
@@ -375,7 +411,6 @@ int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_par
 int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float* tokens,
                        const float* stats_in, float* stats_out, const fs_points* out,
                        void* workspace, size_t workspace_bytes, void* stream) {
-  (void)workspace; (void)workspace_bytes;
   const char* who = "fs_deslice_fwd";
   int32_t rc = check_params(p, who);
   if (!rc) rc = check_points(x, "x_mid", p->D, who);
@@ -383,6 +418,9 @@ int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float
   if (rc) return rc;
   if (out->dtype != x->dtype) return fail(FS_ERR_INVALID, "%s: out and x_mid dtypes differ", who);
   if (!tokens) return fail(FS_ERR_INVALID, "%s: tokens is NULL", who);
+  const Workspace ws = plan_ws(FS_OP_DESLICE_FWD, p, (char*)workspace);
+  rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
+  if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
   const int mode = mode_of(p->dot, x->dtype);
   if (family_of(p) == 1) {
@@ -405,6 +443,8 @@ int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float
   a.vec_1 = vec_ok(out);
   a.fast = a.vec_x && a.vec_1 && full_widths(p);
   a.tok = tokens;
+  rc = gp_prepare(a, p, ws, mode, st, who);
+  if (rc) return rc;
   if (stats_in) {
     a.stats_in = stats_in;
     return hip_check(fs::launch_blocked(fs::BK_DESLICE_N, a, x->dtype, mode, st), who);
@@ -459,12 +499,6 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     rs.seg[1] = seg(ws.part, wf, (int64_t)G * D, pb(g), G, Bb, Hb, dbias);
     rs.seg[2] = seg(ws.part, wf, (int64_t)G * D + G, pb(g), 1, 1, (int)p->H, dtau);
   } else {
-    const float* stats = stats_in;
-    if (!stats) {
-      rc = run_stats(x, p, ws.stats, 0, st, who);
-      if (rc) return rc;
-      stats = ws.stats;
-    }
     const Geo gn = geo_n(p, 512), gg = geo_g(p);
     fs::Args a = base_args(p, gn);
     set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
@@ -478,6 +512,14 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     a.fast = a.vec_x && a.vec_f && a.vec_1 && a.vec_2 && full_widths(p);
     a.tok = dz_num;
     a.ds = ds;
+    rc = gp_prepare(a, p, ws, mode, st, who);
+    if (rc) return rc;
+    const float* stats = stats_in;
+    if (!stats) {
+      rc = run_stats(x, p, ws.stats, 0, a, st, who);
+      if (rc) return rc;
+      stats = ws.stats;
+    }
     a.stats_in = stats;
     a.delta = ws.delta;
     a.lsum = ws.lsum;
@@ -542,11 +584,6 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
     rs.seg[3] = seg(ws.part, wf, offB + G, pb(g), 1, 1, (int)p->H, dtau);
   } else {
     const float* stats = stats_in;
-    if (!stats) {
-      rc = run_stats(x, p, ws.stats, 0, st, who);
-      if (rc) return rc;
-      stats = ws.stats;
-    }
     const Geo gn = geo_n(p, 512), gg = geo_g(p);
     fs::Args a = base_args(p, gn);
     set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
@@ -557,6 +594,13 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
     a.vec_1 = vec_ok(dx);
     a.fast = a.vec_x && a.vec_f && a.vec_1 && full_widths(p);
     a.tok = tokens;
+    rc = gp_prepare(a, p, ws, mode, st, who);
+    if (rc) return rc;
+    if (!stats) {
+      rc = run_stats(x, p, ws.stats, 0, a, st, who);
+      if (rc) return rc;
+      stats = ws.stats;
+    }
     a.stats_in = stats;
     a.delta = ws.delta;
     a.lsum = ws.lsum;

@@ -23,6 +23,17 @@ static hipError_t blocked_dispatch(const Args& a, int dtype, int mode, hipStream
   return blocked_launch<K, _Float16, 0>(a, st);
 }
 
+hipError_t launch_gp_prep(const Args& a, int mode, hipStream_t st) {
+  const dim3 grid((a.G + 31) / 32, a.B * a.H, 6), blk(256);
+  if (mode == 1)
+    hipLaunchKernelGGL(k_gp_prep<1>, grid, blk, 0, st, a);
+  else if (mode == 2)
+    hipLaunchKernelGGL(k_gp_prep<2>, grid, blk, 0, st, a);
+  else
+    hipLaunchKernelGGL(k_gp_prep<0>, grid, blk, 0, st, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_blocked(int kind, const Args& a, int dtype, int mode, hipStream_t st) {
   switch (kind) {
     case BK_STATS: return blocked_dispatch<BK_STATS>(a, dtype, mode, st);

@@ -24,6 +24,7 @@
 // (:576-673), _slice_bwd_g_kernel (:676-741), _deslice_bwd_n_kernel
 // (:744-815), _deslice_bwd_g_kernel (:818-888).
 #pragma once
+#include "fs_gp_kernels.h"
 #include "fs_tile.h"
 
 namespace fs {
@@ -606,6 +607,34 @@ hipError_t blocked_launch(const Args& a, hipStream_t st) {
   const int bh = a.B * a.H;
   const dim3 gn(a.P / kWavesPerBlock, bh), gg(a.P / kWavesPerBlock, bh, (a.G + 31) / 32);
   const dim3 blk(256);
+  if (gp_serves(a.D, a.DV)) {
+    // prepared-fragment kernels (fs_gp_kernels.h); slot-owned grids run the
+    // slot blocks fastest
+    const dim3 gq((a.G + 31) / 32, a.P / kWavesPerBlock, bh);
+#define GP_TRY(NB_)                                                                            \
+    if (NBc == NB_) {                                                                          \
+      if constexpr (K == BK_STATS)                                                             \
+        hipLaunchKernelGGL((k_gp_stats<T, DK, NB_>), gn, blk, 0, st, a);                       \
+      else if constexpr (K == BK_DESLICE_N)                                                    \
+        hipLaunchKernelGGL((k_gp_deslice<T, DK, NB_, false>), gn, blk, 0, st, a);              \
+      else if constexpr (K == BK_DESLICE_ONLINE)                                               \
+        hipLaunchKernelGGL((k_gp_deslice<T, DK, NB_, true>), gn, blk, 0, st, a);               \
+      else if constexpr (K == BK_SLICE_G)                                                      \
+        hipLaunchKernelGGL((k_gp_slice_g<T, DK, NB_>), gq, blk, 0, st, a);                     \
+      else if constexpr (K == BK_SLICE_BWD_N)                                                  \
+        hipLaunchKernelGGL((k_gp_bwd_n<T, DK, NB_, true>), gn, blk, 0, st, a);                 \
+      else if constexpr (K == BK_SLICE_BWD_G)                                                  \
+        hipLaunchKernelGGL((k_gp_bwd_g<T, DK, NB_, true>), gq, blk, 0, st, a);                 \
+      else if constexpr (K == BK_DESLICE_BWD_N)                                                \
+        hipLaunchKernelGGL((k_gp_bwd_n<T, DK, NB_, false>), gn, blk, 0, st, a);                \
+      else                                                                                     \
+        hipLaunchKernelGGL((k_gp_bwd_g<T, DK, NB_, false>), gq, blk, 0, st, a);                \
+      return hipGetLastError();                                                                \
+    }
+    GP_TRY(1) GP_TRY(2)
+#undef GP_TRY
+    return hipErrorNotSupported;
+  }
 #define BK_TRY(NB_)                                                                            \
   if (NBc == NB_) {                                                                            \
     if constexpr (K == BK_STATS)                                                               \

@@ -36,7 +36,47 @@ struct Args {
   int fast;                                // all rows aligned, D and DV multiples of 32
   int nd, nv;                              // 32-wide blocks of D and DV (blocked family)
   int two_pass;                            // statistics: max pass, then sum pass
+  // G-blocked family, widths up to 64: operand fragments and per-slot
+  // vectors prepared once per call (k_gp_prep) at u32x4 offsets foff[kind]
+  // of `frags` (gp_layout)
+  void* frags;
+  int64_t foff[6];
 };
+
+// Kinds of prepared fragments (G-blocked family): W [g-outer, d-inner] in the
+// logits mode; W / tau [d-outer, g-inner], V [g-outer, v-inner] and V
+// [v-outer, g-inner] (V = tokens or dz_num) in the value mode; and two
+// per-slot vectors in lane-ready form (4 u32x4 per lane: lane half h's 16
+// values of slots kmap(j, h)): bias * log2(e) / tau (-1e30 beyond G) and d s
+// (0 beyond G). Item k of slot block gb of head bh is at foff[kind] +
+// ((bh * ngb + gb) * nk + k) * FW (nk = blocks of D or DV, or 1 for the
+// vectors; FW = u32x4 per item).
+enum GpKind { GP_WR = 0, GP_WC = 1, GP_VR = 2, GP_VC = 3, GP_BC = 4, GP_DS = 5 };
+struct GpLayout {
+  int64_t off[6];
+  int64_t total_u32x4;
+};
+// u32x4 per 32 x 32 fragment in the dot kind's logits / value mode
+__host__ __device__ inline int gp_fw(int dk, bool logits) {
+  const bool x6 = logits ? dk != 2 : dk == 0;
+  return (x6 ? 6 : 2) * 64;
+}
+constexpr int kGpVecFw = 4 * 64;  // u32x4 per per-slot vector item
+__host__ __device__ inline GpLayout gp_layout(int B, int H, int G, int D, int DV, int dk) {
+  GpLayout l;
+  const int64_t bhg = (int64_t)B * H * ((G + 31) / 32);
+  const int64_t nd = (D + 31) / 32, nv = (DV + 31) / 32;
+  l.off[GP_WR] = 0;
+  l.off[GP_WC] = l.off[GP_WR] + bhg * nd * gp_fw(dk, true);
+  l.off[GP_VR] = l.off[GP_WC] + bhg * nd * gp_fw(dk, false);
+  l.off[GP_VC] = l.off[GP_VR] + bhg * nv * gp_fw(dk, false);
+  l.off[GP_BC] = l.off[GP_VC] + bhg * nv * gp_fw(dk, false);
+  l.off[GP_DS] = l.off[GP_BC] + bhg * kGpVecFw;
+  l.total_u32x4 = l.off[GP_DS] + bhg * kGpVecFw;
+  return l;
+}
+// the prepared-fragment kernels serve D, DV <= 64 (older kernels above)
+__host__ __device__ inline bool gp_serves(int D, int DV) { return D <= 64 && DV <= 64; }
 
 // Partial-buffer layout of one wave (floats), fused family:
 //   slice fwd:   z [G][DV], s [G]
@@ -73,6 +113,8 @@ enum BlockedKind {
   BK_DESLICE_BWD_G = 7   // dtokens, dW, db partials
 };
 hipError_t launch_blocked(int kind, const Args& a, int dtype, int mode, hipStream_t st);
+// builds a.frags / a.fvec for the G-blocked kernels of one call (gp_serves)
+hipError_t launch_gp_prep(const Args& a, int mode, hipStream_t st);
 int blocked_width_blocks(int D, int DV);  // 1, 2, 4 or 8 (0 if D or DV > 256)
 
 // Deterministic reduction of per-wave partials (fs_reduce.hip). One output

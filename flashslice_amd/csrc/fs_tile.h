@@ -214,4 +214,34 @@ __device__ __forceinline__ void copy_frags(float (&dst)[NB][16], const float (&s
     for (int j = 0; j < 16; ++j) dst[k][j] = src[k][j];
 }
 
+// The tile loop of the point-streaming kernels (wave pid owns tiles pid,
+// pid + a.P, ...): two register sets of point
+// rows alternate, each reloaded (two tiles ahead) right after the tile it
+// held is computed, so no registers are copied between iterations. The first
+// pass is peeled so that the loop is entered with the same memory operations
+// outstanding as on every back edge: the compiler then waits only for the
+// rows a tile needs, never for the stores still in flight. A load beyond the
+// last tile reads an empty range (zeros, no memory traffic).
+#define FS_TILE_LOOP(LOAD, BODY, A_ARGS, B_ARGS)                                          \
+  {                                                                                       \
+    int t_ = pid;                                                                         \
+    LOAD(A_ARGS, t_);                                                                     \
+    LOAD(B_ARGS, t_ + a.P);                                                               \
+    if (t_ < a.ntiles) {                                                                  \
+      BODY(A_ARGS, t_);                                                                   \
+      LOAD(A_ARGS, t_ + 2 * a.P);                                                         \
+      t_ += a.P;                                                                          \
+      while (t_ < a.ntiles) {                                                             \
+        BODY(B_ARGS, t_);                                                                 \
+        LOAD(B_ARGS, t_ + 2 * a.P);                                                       \
+        t_ += a.P;                                                                        \
+        if (t_ >= a.ntiles) break;                                                        \
+        BODY(A_ARGS, t_);                                                                 \
+        LOAD(A_ARGS, t_ + 2 * a.P);                                                       \
+        t_ += a.P;                                                                        \
+      }                                                                                   \
+    }                                                                                     \
+  }
+#define FS_ARGS2(X, Y) X, Y
+
 }  // namespace fs

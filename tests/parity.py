@@ -8,9 +8,10 @@ Gates (reference ``bench/parity_ops.py:51-55, 189-206``):
     2x for dtau on G-blocked shapes;
   * bf16 dot modes: within 2x of eager-on-bf16-inputs' error (+1e-6);
   * the north-star bound for fp32 ieee: relerr(fused, eager fp32) <= 1e-5
-    for every output whose eager error is itself below 1e-5 (dtau and db
-    are cancellation sums whose eager error can exceed it; they are held to
-    the ratio gate);
+    (+ eager's own error against float64, which a more accurate result may
+    sit across from) for every output whose eager error is itself below
+    1e-5; outputs whose eager error exceeds it (cancellation sums such as
+    dtau and db at large N) are held to the ratio gate;
   * shapes and dtypes of every output and gradient equal the eager ones;
   * two fused runs are bitwise identical.
 """
@@ -141,7 +142,10 @@ def check_case(case, order="slice-first", dot="", kernel_mode="auto", gate=1.25,
             ok = ef <= 2.0 * ee + 1e-6
         else:
             ok = ef <= g * ee + 1e-6 or (ee > 1e-4 and ef <= 3.0 * ee)
-            if strict and ok and ee < 1e-5 and fe > 1e-5:
+            # fused vs eager within 1e-5, up to eager's own distance from the
+            # float64 truth (a result closer to the truth than eager can sit
+            # on the other side of it: fe <= ef + ee)
+            if strict and ok and ee < 1e-5 and fe > 1e-5 + ee:
                 ok = False
         if not ok:
             fails.append("%s: eager %.3e fused %.3e fused-vs-eager %.3e" % (k, ee, ef, fe))
