@@ -303,7 +303,7 @@ __global__ __launch_bounds__(256, 2) void k_blk_slice_g(Args a) {
   for (int k = 0; k < NB; ++k) zacc[k] = zero16();
   const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
   const T* fb = (const T*)a.f + b * a.sfb + hd * a.sfh;
-  for (int t = pid; t < a.ntiles; t += a.P) {
+  for (int t = pid, it = 0; t < a.ntiles; t += a.P, ++it) {
     const int p0 = t * kTile, p = p0 + c;
     const bool pv = p < N;
     float xf[NB][16];
@@ -320,18 +320,19 @@ __global__ __launch_bounds__(256, 2) void k_blk_slice_g(Args a) {
     load_stats(m2, l, a.stats_in, bh, N, p);
     float t2[16], w[16];
     blk_logits<ML, NB>(t2, wA, xf, bc, cst, nd);
-    const float inv_l = pv ? 1.f / l : 0.f;
+    const float sg = tile_sign(it);  // the weights carry the tile's sign (acc_add)
+    const float inv_l = pv ? sg / l : 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) w[r] = __builtin_amdgcn_exp2f(t2[r] - m2) * inv_l;
     float wT[16];
     transpose32(wT, w, lds, c, h);
 #pragma unroll
     for (int k = 0; k < NB; ++k)
-      if (k < nv) zacc[k] = mma32<MV>(fT[k], wT, zacc[k]);
+      if (k < nv) mma32_acc<MV>(zacc[k], fT[k], wT, sg);
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) s += wT[j];
-    sacc += s;
+    sacc = fmaf(s, sg, sacc);
   }
   float* pw = a.part + ((int64_t)bh * a.P + pid) * part_floats_slice_fwd(G, DV);
   const int g = g0 + c;
@@ -513,7 +514,7 @@ __global__ __launch_bounds__(256, 2) void k_blk_bwd_g(Args a) {
   }
   const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
   const T* fb = (const T*)a.f + b * a.sfb + hd * a.sfh;
-  for (int t = pid; t < a.ntiles; t += a.P) {
+  for (int t = pid, it = 0; t < a.ntiles; t += a.P, ++it) {
     const int p = t * kTile + c;
     const bool pv = p < N;
     float xf[NB][16], ff[NB][16];
@@ -525,7 +526,9 @@ __global__ __launch_bounds__(256, 2) void k_blk_bwd_g(Args a) {
     const float delta = load_delta(a.delta, bh, N, p);
     float t2[16], w[16];
     blk_logits<ML, NB>(t2, wA, xf, bc, cst, nd);
-    const float inv_l = pv ? 1.f / l : 0.f;
+    // the weights -- and through them Lb -- carry the tile's sign (acc_add)
+    const float sg = tile_sign(it);
+    const float inv_l = pv ? sg / l : 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) w[r] = __builtin_amdgcn_exp2f(t2[r] - m2) * inv_l;
     if (!SLICE) {
@@ -537,7 +540,7 @@ __global__ __launch_bounds__(256, 2) void k_blk_bwd_g(Args a) {
         if (k < nv) {
           float oT[16];
           transpose32(oT, ff[k], lds, c, h);
-          dT[k] = mma32<MV>(oT, wT, dT[k]);
+          mma32_acc<MV>(dT[k], oT, wT, sg);
         }
     }
     f32x16 o = zero16();
@@ -554,12 +557,12 @@ __global__ __launch_bounds__(256, 2) void k_blk_bwd_g(Args a) {
       if (k < nd) {
         float xT[16];
         transpose32(xT, xf[k], lds, c, h);
-        dW[k] = mma32<MV>(xT, aT, dW[k]);
+        mma32_acc<MV>(dW[k], xT, aT, sg);
       }
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) s += aT[j];
-    dbacc += s;
+    dbacc = fmaf(s, sg, dbacc);
   }
   const int g = g0 + c;
   const float s = dbacc + xor32(dbacc);

@@ -70,6 +70,33 @@ __device__ __forceinline__ f32x16 mma32(const float (&a)[16], const float (&b)[1
   return c;
 }
 
+// Accumulators that run over a wave's whole stream of point tiles (z_num,
+// dtokens, dW) are kept free of the bf16 MFMA's rounding bias. On MI355X the
+// MFMA sums its products with a small downward bias when they span many
+// binades (softmax weights do): measured at about -0.03 x 2^-24 x the largest
+// product per MFMA, the same with an operand negated. Chained over hundreds
+// of tiles, and through an accumulator whose magnitude keeps growing, that
+// bias shifted every slot's z_num by the same few 1e-6 (relative) at
+// N = 1e6. Hence:
+//   * each tile's block is summed by the MFMAs from zero and added to acc in
+//     fp32 (round to nearest even), so the bias is relative to one tile's
+//     sum, not to the running total;
+//   * every other tile negates one MFMA operand and subtracts its block
+//     (`sgn` = -1): the bias then enters with alternating signs and cancels
+//     while the values add up unchanged (t * -1 is exact; fma(t, -1, acc) is
+//     the correctly rounded acc - t).
+// `tile_sign` gives the sign for a wave's i-th tile.
+__device__ __forceinline__ float tile_sign(int i) { return (i & 1) ? -1.f : 1.f; }
+__device__ __forceinline__ void acc_add(f32x16& acc, const f32x16& t, float sgn) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = fmaf(t[i], sgn, acc[i]);
+}
+template <int MODE>
+__device__ __forceinline__ void mma32_acc(f32x16& acc, const float (&a)[16], const float (&b)[16],
+                                          float sgn) {
+  acc_add(acc, mma32<MODE>(a, b, zero16()), sgn);
+}
+
 // ---------------------------------------------------------------- dtype I/O
 template <typename T> __device__ __forceinline__ float to_f(T v);
 template <> __device__ __forceinline__ float to_f<float>(float v) { return v; }

@@ -198,9 +198,11 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
 #pragma unroll
       for (int vb = 0; vb < NVB; ++vb) ld_cols<T>(fn[vb], rf, vcf[vb], (uint32_t)f_sn);
     };
+    int it = 0;
     auto body = [&](const float (&xf)[NDB][16], const float (&fT)[NVB][16], int t) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
+      const float sg = tile_sign(it++);
       float t2[NGB][16], w[NGB][16], m2, lsum;
       {
         Frag<ML> xq[NDB];
@@ -210,9 +212,14 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
       }
       softmax_tile<NGB>(w, m2, lsum, t2, pv);
       store_stats_tile(st_m, st_l, p0, N, c, h, m2, lsum);
-      Frag<MV> fq[NVB];
+      Frag<MV> fq[NVB];  // fx carries the tile's sign (acc_add)
 #pragma unroll
-      for (int vb = 0; vb < NVB; ++vb) prep<MV>(fq[vb], fT[vb]);
+      for (int vb = 0; vb < NVB; ++vb) {
+        float fs[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) fs[j] = fT[vb][j] * sg;
+        prep<MV>(fq[vb], fs);
+      }
 #pragma unroll
       for (int gb = 0; gb < NGB; ++gb) {
         float wT[16];
@@ -220,7 +227,7 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
         Frag<MV> wq;
         prep<MV>(wq, wT);
 #pragma unroll
-        for (int vb = 0; vb < NVB; ++vb) zacc[gb][vb] = mma<MV>(fq[vb], wq, zacc[gb][vb]);
+        for (int vb = 0; vb < NVB; ++vb) mma_acc<MV>(zacc[gb][vb], fq[vb], wq, sg);
         float s = 0.f;
 #pragma unroll
         for (int j = 0; j < 16; ++j) s += wT[j];
@@ -315,8 +322,9 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
 // dx = Lb (W / tau) and dW += Lb^T x, db += sum_n Lb (scaled by 1 / tau
 // when the partials are written) for the two backward kernels: `om` holds
 // Lb ([point-outer, slot-inner]); qWc the ready fragments of W / tau as
-// [d-outer, g-inner] (index db * NGB + gb).
-#define FS_DX_DW(OM, QWC)                                                           \
+// [d-outer, g-inner] (index db * NGB + gb); x^T carries the tile's sign SG
+// (acc_add).
+#define FS_DX_DW(OM, QWC, SG)                                                       \
   {                                                                                 \
     f32x16 o_[NDB];                                                                 \
     _Pragma("unroll") for (int db = 0; db < NDB; ++db) o_[db] = zero16();           \
@@ -338,6 +346,7 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
     _Pragma("unroll") for (int db = 0; db < NDB; ++db) {                            \
       float xT_[16];                                                                \
       transpose32(xT_, xf[db], lds, c, h);                                          \
+      _Pragma("unroll") for (int j = 0; j < 16; ++j) xT_[j] *= (SG);                \
       prep<MV>(xTq_[db], xT_);                                                      \
     }                                                                               \
     _Pragma("unroll") for (int gb = 0; gb < NGB; ++gb) {                            \
@@ -346,7 +355,7 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
       Frag<MV> aTq_;                                                                \
       prep<MV>(aTq_, aT_);                                                          \
       _Pragma("unroll") for (int db = 0; db < NDB; ++db)                            \
-        dW[gb][db] = mma<MV>(xTq_[db], aTq_, dW[gb][db]);                           \
+        mma_acc<MV>(dW[gb][db], xTq_[db], aTq_, (SG));                              \
       float s_ = 0.f;                                                               \
       _Pragma("unroll") for (int j = 0; j < 16; ++j) s_ += aT_[j];                  \
       dbacc[gb] += s_;                                                              \
@@ -406,9 +415,11 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
     auto load_f = [&](int t) {
       ld_rows<T, NVB, FAST>(ff, rows_rsrc(f_b, f_sn, f_w, (int64_t)t * kTile, N), vrf, DV, h);
     };
+    int it = 0;
     auto body = [&](const float (&xf)[NDB][16], int t) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
+      const float sg = tile_sign(it++);
       float t2[NGB][16], w[NGB][16], m2, lsum;
       {
         Frag<ML> xq[NDB];
@@ -461,7 +472,7 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
         for (int vb = 0; vb < NVB; ++vb) st_cols<T>(rdf, vcf[vb], (uint32_t)df_sn, o[vb]);
       }
       dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
-      FS_DX_DW(om, qWc)
+      FS_DX_DW(om, qWc, sg)
     };
     load_f(pid);
     FS_TILE_LOOP(load, body, xA, xB)
@@ -539,9 +550,11 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
     auto load_g = [&](int t) {
       ld_rows<T, NVB, FAST>(of, rows_rsrc(g_b, g_sn, g_w, (int64_t)t * kTile, N), vrg, DV, h);
     };
+    int it = 0;
     auto body = [&](const float (&xf)[NDB][16], int t) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
+      const float sg = tile_sign(it++);
       float t2[NGB][16], w[NGB][16], m2, lsum;
       {
         Frag<ML> xq[NDB];
@@ -569,11 +582,13 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
           from16(om[gb], o);
         }
       }
-      Frag<MV> oTq[NVB];
+      Frag<MV> oTq[NVB];  // d_out^T carries the tile's sign (acc_add)
 #pragma unroll
       for (int vb = 0; vb < NVB; ++vb) {
         float oT[16];
         transpose32(oT, of[vb], lds, c, h);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) oT[j] *= sg;
         prep<MV>(oTq[vb], oT);
       }
       load_g(t + a.P);
@@ -586,10 +601,10 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
         Frag<MV> wTq;
         prep<MV>(wTq, wT);
 #pragma unroll
-        for (int vb = 0; vb < NVB; ++vb) dT[gb][vb] = mma<MV>(oTq[vb], wTq, dT[gb][vb]);
+        for (int vb = 0; vb < NVB; ++vb) mma_acc<MV>(dT[gb][vb], oTq[vb], wTq, sg);
       }
       dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
-      FS_DX_DW(om, qWc)
+      FS_DX_DW(om, qWc, sg)
     };
     load_g(pid);
     FS_TILE_LOOP(load, body, xA, xB)

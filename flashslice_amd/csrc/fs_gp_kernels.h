@@ -427,6 +427,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_slice_g(Args a) {
 #pragma unroll
       for (int k = 0; k < NB; ++k) ld_cols<T>(fn[k], rf, vcf[k], (uint32_t)f_sn);
     };
+    int it = 0;
     auto body = [&](const float (&xf)[NB][16], const float (&fT)[NB][16], int t) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
@@ -437,7 +438,9 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_slice_g(Args a) {
       for (int k = 0; k < NB; ++k) prep<ML>(xq[k], xf[k]);
       float t2[16], w[16];
       gp_logits<ML, NB>(t2, sq, sq + NB * FWL, xq, nd, cst, lane);
-      const float inv_l = pv ? 1.f / l : 0.f;
+      // the weights carry the tile's sign (acc_add)
+      const float sg = tile_sign(it++);
+      const float inv_l = pv ? sg / l : 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) w[r] = __builtin_amdgcn_exp2f(t2[r] - m2) * inv_l;
       float wT[16];
@@ -449,12 +452,12 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_slice_g(Args a) {
         if (k < nv) {
           Frag<MV> fq;
           prep<MV>(fq, fT[k]);
-          zacc[k] = mma<MV>(fq, wq, zacc[k]);
+          mma_acc<MV>(zacc[k], fq, wq, sg);
         }
       float s = 0.f;
 #pragma unroll
       for (int j = 0; j < 16; ++j) s += wT[j];
-      sacc += s;
+      sacc = fmaf(s, sg, sacc);
     };
     FS_TILE_LOOP(load, body, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
   };
@@ -685,6 +688,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_bwd_g(Args a) {
       ld_rows<T, NB, FAST>(xn, rows_rsrc(x_b, x_sn, x_w, p0, N), vrx, D, h);
       ld_rows<T, NB, FAST>(fn, rows_rsrc(f_b, f_sn, f_w, p0, N), vrf, DV, h);
     };
+    int it = 0;
     auto body = [&](const float (&xf)[NB][16], const float (&ff)[NB][16], int t) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
@@ -696,7 +700,9 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_bwd_g(Args a) {
       for (int k = 0; k < NB; ++k) prep<ML>(xq[k], xf[k]);
       float t2[16], w[16];
       gp_logits<ML, NB>(t2, sq, sq + O_BC, xq, nd, cst, lane);
-      const float inv_l = pv ? 1.f / l : 0.f;
+      // the weights -- and through them Lb -- carry the tile's sign (acc_add)
+      const float sg = tile_sign(it++);
+      const float inv_l = pv ? sg / l : 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) w[r] = __builtin_amdgcn_exp2f(t2[r] - m2) * inv_l;
       if (!SLICE) {
@@ -712,7 +718,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_bwd_g(Args a) {
             transpose32(oT, ff[k], lds, c, h);
             Frag<MV> oq;
             prep<MV>(oq, oT);
-            dT[k] = mma<MV>(oq, wq, dT[k]);
+            mma_acc<MV>(dT[k], oq, wq, sg);
           }
       }
       f32x16 o = zero16();
@@ -740,12 +746,12 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_bwd_g(Args a) {
           transpose32(xT, xf[k], lds, c, h);
           Frag<MV> xtq;
           prep<MV>(xtq, xT);
-          dW[k] = mma<MV>(xtq, aq, dW[k]);
+          mma_acc<MV>(dW[k], xtq, aq, sg);
         }
       float s = 0.f;
 #pragma unroll
       for (int j = 0; j < 16; ++j) s += aT[j];
-      dbacc += s;
+      dbacc = fmaf(s, sg, dbacc);
     };
     FS_TILE_LOOP(load, body, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
   };

@@ -150,6 +150,15 @@ __device__ __forceinline__ f32x16 mma<MMA_X6>(const Frag<MMA_X6>& a, const Frag<
   return c;
 }
 
+// acc += sgn (A B) over one contraction block for an accumulator that runs
+// over many point tiles (summed from zero, then added in fp32; the caller
+// has negated one operand when sgn = -1: acc_add).
+template <int M>
+__device__ __forceinline__ void mma_acc(f32x16& acc, const Frag<M>& a, const Frag<M>& b,
+                                        float sgn) {
+  acc_add(acc, mma<M>(a, b, zero16()), sgn);
+}
+
 // Ready fragments in LDS: word w of lane l at slot[w * 64 + l] (16-byte
 // words; a wave reads or writes 1 KB of consecutive words per instruction,
 // conflict-free).

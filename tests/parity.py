@@ -107,12 +107,15 @@ class Case:
 
 
 def check_case(case, order="slice-first", dot="", kernel_mode="auto", gate=1.25,
-               blocked=False, grads=True, strict=True):
+               blocked=False, grads=True, strict=True, ref_device="cpu"):
     """Run ``case`` through the oracle (fp64, fp32) and the HIP path twice;
-    return a list of failure strings (empty = pass) and the metrics."""
+    return a list of failure strings (empty = pass) and the metrics.
+    ``ref_device``: where the oracle's tensors live (the full-size cases
+    evaluate the same restatement on the GPU's ATen kernels)."""
     amp = dot in ("bf16", "bf16v")
-    ref = case.run(torch.float64, fused=False, order=order, grads=grads)
-    ea = case.run(torch.float32, fused=False, amp=amp, order=order, grads=grads)
+    ref = case.run(torch.float64, fused=False, device=ref_device, order=order, grads=grads)
+    ea = case.run(torch.float32, fused=False, device=ref_device, amp=amp, order=order,
+                  grads=grads)
     set_kernel_mode(kernel_mode)
     set_dot_mode(dot)
     try:
