@@ -85,8 +85,17 @@ __device__ __forceinline__ f32x16 mma32(const float (&a)[16], const float (&b)[1
 //     (`sgn` = -1): the bias then enters with alternating signs and cancels
 //     while the values add up unchanged (t * -1 is exact; fma(t, -1, acc) is
 //     the correctly rounded acc - t).
-// `tile_sign` gives the sign for a wave's i-th tile.
+// `tile_sign` gives the sign for a wave's i-th tile; the ping-pong tile loop
+// (FS_TILE_LOOP) hands its bodies the parity as a type (TileEven / TileOdd)
+// instead, so that the sign folds into the code (negation as a source
+// modifier, fma(t, -1, acc) as a subtraction).
 __device__ __forceinline__ float tile_sign(int i) { return (i & 1) ? -1.f : 1.f; }
+struct TileEven {
+  static constexpr float sign = 1.f;
+};
+struct TileOdd {
+  static constexpr float sign = -1.f;
+};
 __device__ __forceinline__ void acc_add(f32x16& acc, const f32x16& t, float sgn) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = fmaf(t[i], sgn, acc[i]);

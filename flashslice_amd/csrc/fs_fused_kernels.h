@@ -198,11 +198,10 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
 #pragma unroll
       for (int vb = 0; vb < NVB; ++vb) ld_cols<T>(fn[vb], rf, vcf[vb], (uint32_t)f_sn);
     };
-    int it = 0;
-    auto body = [&](const float (&xf)[NDB][16], const float (&fT)[NVB][16], int t) {
+    auto body = [&](const float (&xf)[NDB][16], const float (&fT)[NVB][16], int t, auto par) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
-      const float sg = tile_sign(it++);
+      constexpr float sg = decltype(par)::sign;
       float t2[NGB][16], w[NGB][16], m2, lsum;
       {
         Frag<ML> xq[NDB];
@@ -284,7 +283,7 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
     auto load = [&](float (&xn)[NDB][16], int t) {
       ld_rows<T, NDB, FAST>(xn, rows_rsrc(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
     };
-    auto body = [&](const float (&xf)[NDB][16], int t) {
+    auto body = [&](const float (&xf)[NDB][16], int t, auto par) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
       float t2[NGB][16], w[NGB][16], m2, lsum;
@@ -415,11 +414,10 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
     auto load_f = [&](int t) {
       ld_rows<T, NVB, FAST>(ff, rows_rsrc(f_b, f_sn, f_w, (int64_t)t * kTile, N), vrf, DV, h);
     };
-    int it = 0;
-    auto body = [&](const float (&xf)[NDB][16], int t) {
+    auto body = [&](const float (&xf)[NDB][16], int t, auto par) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
-      const float sg = tile_sign(it++);
+      constexpr float sg = decltype(par)::sign;
       float t2[NGB][16], w[NGB][16], m2, lsum;
       {
         Frag<ML> xq[NDB];
@@ -550,11 +548,10 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
     auto load_g = [&](int t) {
       ld_rows<T, NVB, FAST>(of, rows_rsrc(g_b, g_sn, g_w, (int64_t)t * kTile, N), vrg, DV, h);
     };
-    int it = 0;
-    auto body = [&](const float (&xf)[NDB][16], int t) {
+    auto body = [&](const float (&xf)[NDB][16], int t, auto par) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
-      const float sg = tile_sign(it++);
+      constexpr float sg = decltype(par)::sign;
       float t2[NGB][16], w[NGB][16], m2, lsum;
       {
         Frag<ML> xq[NDB];
@@ -582,14 +579,17 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
           from16(om[gb], o);
         }
       }
-      Frag<MV> oTq[NVB];  // d_out^T carries the tile's sign (acc_add)
+      // d_out^T, carrying the tile's sign (acc_add); split into MFMA pieces
+      // here when several slot blocks share it, else next to its one use
+      // (16 registers across the softmax instead of the split's 24)
+      float oT[NVB][16];
+      Frag<MV> oTq[NVB];
 #pragma unroll
       for (int vb = 0; vb < NVB; ++vb) {
-        float oT[16];
-        transpose32(oT, of[vb], lds, c, h);
+        transpose32(oT[vb], of[vb], lds, c, h);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) oT[j] *= sg;
-        prep<MV>(oTq[vb], oT);
+        for (int j = 0; j < 16; ++j) oT[vb][j] *= sg;
+        if constexpr (NGB > 1) prep<MV>(oTq[vb], oT[vb]);
       }
       load_g(t + a.P);
       softmax_tile<NGB>(w, m2, lsum, t2, pv);
@@ -601,7 +601,10 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
         Frag<MV> wTq;
         prep<MV>(wTq, wT);
 #pragma unroll
-        for (int vb = 0; vb < NVB; ++vb) mma_acc<MV>(dT[gb][vb], oTq[vb], wTq, sg);
+        for (int vb = 0; vb < NVB; ++vb) {
+          if constexpr (NGB == 1) prep<MV>(oTq[vb], oT[vb]);
+          mma_acc<MV>(dT[gb][vb], oTq[vb], wTq, sg);
+        }
       }
       dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
       FS_DX_DW(om, qWc, sg)

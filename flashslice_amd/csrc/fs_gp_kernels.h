@@ -427,8 +427,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_slice_g(Args a) {
 #pragma unroll
       for (int k = 0; k < NB; ++k) ld_cols<T>(fn[k], rf, vcf[k], (uint32_t)f_sn);
     };
-    int it = 0;
-    auto body = [&](const float (&xf)[NB][16], const float (&fT)[NB][16], int t) {
+    auto body = [&](const float (&xf)[NB][16], const float (&fT)[NB][16], int t, auto par) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
       const float m2 = ld_pt(pts_rsrc(sm, p0, N), c) * kLog2e;
@@ -439,7 +438,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_slice_g(Args a) {
       float t2[16], w[16];
       gp_logits<ML, NB>(t2, sq, sq + NB * FWL, xq, nd, cst, lane);
       // the weights carry the tile's sign (acc_add)
-      const float sg = tile_sign(it++);
+      constexpr float sg = decltype(par)::sign;
       const float inv_l = pv ? sg / l : 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) w[r] = __builtin_amdgcn_exp2f(t2[r] - m2) * inv_l;
@@ -688,8 +687,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_bwd_g(Args a) {
       ld_rows<T, NB, FAST>(xn, rows_rsrc(x_b, x_sn, x_w, p0, N), vrx, D, h);
       ld_rows<T, NB, FAST>(fn, rows_rsrc(f_b, f_sn, f_w, p0, N), vrf, DV, h);
     };
-    int it = 0;
-    auto body = [&](const float (&xf)[NB][16], const float (&ff)[NB][16], int t) {
+    auto body = [&](const float (&xf)[NB][16], const float (&ff)[NB][16], int t, auto par) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
       const float m2 = ld_pt(pts_rsrc(sm, p0, N), c) * kLog2e;
@@ -701,7 +699,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_bwd_g(Args a) {
       float t2[16], w[16];
       gp_logits<ML, NB>(t2, sq, sq + O_BC, xq, nd, cst, lane);
       // the weights -- and through them Lb -- carry the tile's sign (acc_add)
-      const float sg = tile_sign(it++);
+      constexpr float sg = decltype(par)::sign;
       const float inv_l = pv ? sg / l : 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) w[r] = __builtin_amdgcn_exp2f(t2[r] - m2) * inv_l;

@@ -228,15 +228,15 @@ __device__ __forceinline__ void copy_frags(float (&dst)[NB][16], const float (&s
     LOAD(A_ARGS, t_);                                                                     \
     LOAD(B_ARGS, t_ + a.P);                                                               \
     if (t_ < a.ntiles) {                                                                  \
-      BODY(A_ARGS, t_);                                                                   \
+      BODY(A_ARGS, t_, TileEven());                                                       \
       LOAD(A_ARGS, t_ + 2 * a.P);                                                         \
       t_ += a.P;                                                                          \
       while (t_ < a.ntiles) {                                                             \
-        BODY(B_ARGS, t_);                                                                 \
+        BODY(B_ARGS, t_, TileOdd());                                                      \
         LOAD(B_ARGS, t_ + 2 * a.P);                                                       \
         t_ += a.P;                                                                        \
         if (t_ >= a.ntiles) break;                                                        \
-        BODY(A_ARGS, t_);                                                                 \
+        BODY(A_ARGS, t_, TileEven());                                                     \
         LOAD(A_ARGS, t_ + 2 * a.P);                                                       \
         t_ += a.P;                                                                        \
       }                                                                                   \
