@@ -38,13 +38,14 @@ template <int DK> struct FModes {
 // LDS of one block (floats): region 0 holds first the fp32 staging of W
 // [32 NGB][SW] and tokens / dz_num [32 NGB][SV] (row strides padded so
 // fragment reads are conflict-free) and, once the ready fragments are
-// built, the four per-wave transpose tiles; then NQL ready fragments of the
-// logits mode and NQV of the value mode; then two per-slot vectors (the
-// scaled bias, and d s in the slice backward).
-template <int NGB, int NDB, int NVB, int ML, int MV, int NQL, int NQV> struct FLds {
+// built, the four per-wave regions of WF floats (a transpose tile, or the
+// regions of split fragments transposed through LDS); then NQL ready
+// fragments of the logits mode and NQV of the value mode; then two per-slot
+// vectors (the scaled bias, and d s in the slice backward).
+template <int NGB, int NDB, int NVB, int ML, int MV, int NQL, int NQV, int WF> struct FLds {
   static constexpr int GP = 32 * NGB;
   static constexpr int SW = 32 * NDB + 4, SV = 32 * NVB + 4;
-  static constexpr int STAGE = GP * SW + GP * SV, TILES = kWavesPerBlock * kLdsTile;
+  static constexpr int STAGE = GP * SW + GP * SV, TILES = kWavesPerBlock * WF;
   static constexpr int R0 = ((STAGE > TILES ? STAGE : TILES) + 3) / 4 * 4;
   static constexpr int QL_OFF = R0;
   static constexpr int QV_OFF = QL_OFF + NQL * frag_words<ML>() * 4;
@@ -97,9 +98,9 @@ __device__ __forceinline__ void acc_put(float& t, float v, bool first) { t = fir
 // [g-outer, d-inner] as ready fragments qL[gb * NDB + db] (bias * log2(e) /
 // tau per output slot in LDS, -1e30 on padded slots). The kernel
 // builds its value-mode fragments next and then calls FS_PROLOGUE_END.
-#define FS_PROLOGUE(NGB, NDB, NVB, NQV)                                             \
+#define FS_PROLOGUE(NGB, NDB, NVB, NQV, WF)                                         \
   constexpr int ML = FModes<DK>::L, MV = FModes<DK>::V;                             \
-  using SM = FLds<NGB, NDB, NVB, ML, MV, NGB * NDB, NQV>;                          \
+  using SM = FLds<NGB, NDB, NVB, ML, MV, NGB * NDB, NQV, (WF)>;                    \
   __shared__ __attribute__((aligned(16))) float smem[SM::TOTAL];                    \
   const int lane = threadIdx.x & 63;                                                \
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);                 \
@@ -110,7 +111,7 @@ __device__ __forceinline__ void acc_put(float& t, float v, bool first) { t = fir
   const int G = a.G, D = a.D, DV = a.DV, N = a.N;                                   \
   float* sW = smem;                                                                 \
   float* sV = smem + SM::GP * SM::SW;                                               \
-  float* lds = smem + wid * kLdsTile;                                               \
+  float* lds = smem + wid * (WF);                                                   \
   u32x4* qL = reinterpret_cast<u32x4*>(smem + SM::QL_OFF);                          \
   u32x4* qV = reinterpret_cast<u32x4*>(smem + SM::QV_OFF);                          \
   float* sBC = smem + SM::VEC_OFF;                                                  \
@@ -169,7 +170,7 @@ constexpr int fused_waves(int ngb, int ndb, int nvb) { return ngb * ndb * nvb ==
 // ------------------------------------------------------------------ slice fwd
 template <typename T, int DK, int NGB, int NDB, int NVB>
 __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice_fwd(Args a) {
-  FS_PROLOGUE(NGB, NDB, NVB, 0)
+  FS_PROLOGUE(NGB, NDB, NVB, 0, kLdsTile)
   FS_PROLOGUE_END
   f32x16 zacc[NGB][NVB];
   float sacc[NGB];
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
 // ---------------------------------------------------------------- deslice fwd
 template <typename T, int DK, int NGB, int NDB, int NVB>
 __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_deslice_fwd(Args a) {
-  FS_PROLOGUE(NGB, NDB, NVB, NVB * NGB)
+  FS_PROLOGUE(NGB, NDB, NVB, NVB * NGB, kLdsTile)
   // tokens as [v-outer, g-inner]: qV[vb * NGB + gb]
   build_frags<MV>(qV, NVB * NGB, wid, lane, [&](int i, float(&f)[16]) {
     lds_frag_colouter(f, sV, SM::SV, 32 * (i % NGB), 32 * (i / NGB), c, h);
@@ -361,10 +362,44 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
     }                                                                               \
   }
 
+// FS_DX_DW for one block of 32 on every axis, from split pieces (TR): Lb is
+// split once, as dx's operand; its pieces, written back with the tile's sign
+// SG and read transposed, give dW's operand and db (their row sums on the
+// matrix cores, the whole tile's sum in both lane halves); x^T comes from the
+// pieces the logits' split left in trX.
+#define FS_DX_DW_TR(OM, QWC, SG)                                                    \
+  {                                                                                 \
+    Frag<MV> aq_;                                                                   \
+    prep<MV>(aq_, OM[0]);                                                           \
+    {                                                                               \
+      Frag<MV> wc_;                                                                 \
+      lds_get<MV>(wc_, QWC, lane);                                                  \
+      const f32x16 o_ = mma<MV>(aq_, wc_, zero16());                                \
+      st_cols<T>(rows_rsrc(dx_b, dx_sn, dx_w, p0, N), vcx[0], (uint32_t)dx_sn, o_);  \
+    }                                                                               \
+    tr_put<MV>(trS, aq_, c, h, (SG) < 0.f ? 0x80008000u : 0u);                      \
+    Frag<MV> aTq_, xTq_;                                                            \
+    tr_get<MV>(aTq_, trS, lane);                                                    \
+    tr_get<MV>(xTq_, trX, lane);                                                    \
+    mma_acc<MV>(dW[0][0], xTq_, aTq_, (SG));                                        \
+    dbacc[0] = fmaf(row_sums<MV>(aTq_)[0], (SG), dbacc[0]);                         \
+  }
+
+// Per-wave LDS of the TR form: x's pieces and one more split fragment.
+template <int DK> constexpr int tr_wave_floats() {
+  return (tr_bytes<FModes<DK>::L>() + tr_bytes<FModes<DK>::V>()) / 4;
+}
+
 // ------------------------------------------------------------------ slice bwd
 template <typename T, int DK, int NGB, int NDB, int NVB>
 __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice_bwd(Args a) {
-  FS_PROLOGUE(NGB, NDB, NVB, 2 * NGB * NVB + NDB * NGB)
+  // TR ((1,1,1), C2): x^T and Lb^T from split pieces read back transposed and
+  // db on the matrix cores (FS_DX_DW_TR): 4 bf16x6 splits per tile instead of 6
+  constexpr bool TR = NGB == 1 && NDB == 1 && NVB == 1;
+  FS_PROLOGUE(NGB, NDB, NVB, 2 * NGB * NVB + NDB * NGB, TR ? tr_wave_floats<DK>() : kLdsTile)
+  char* trX = reinterpret_cast<char*>(lds);
+  char* trS = trX + tr_bytes<ML>();
+  (void)trS;
   // dz_num as [g-outer, v-inner] (omega, qZr[gb * NVB + vb]) and [v-outer,
   // g-inner] (dfx, qZc[vb * NGB + gb]); W as [d-outer, g-inner] (dx).
   u32x4* qZr = qV;
@@ -423,6 +458,7 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
         Frag<ML> xq[NDB];
 #pragma unroll
         for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xf[db]);
+        if constexpr (TR) tr_put<ML>(trX, xq[0], c, h, 0u);
         FS_LOGITS(t2, xq)
       }
       // omega = fx . dz_num + ds (needs no weights: formed first, so that
@@ -470,15 +506,19 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
         for (int vb = 0; vb < NVB; ++vb) st_cols<T>(rdf, vcf[vb], (uint32_t)df_sn, o[vb]);
       }
       dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
-      FS_DX_DW(om, qWc, sg)
+      if constexpr (TR) {
+        FS_DX_DW_TR(om, qWc, sg)
+      } else {
+        FS_DX_DW(om, qWc, sg)
+      }
     };
     load_f(pid);
     FS_TILE_LOOP(load, body, xA, xB)
   };
   if (fast) run(std::true_type()); else run(std::false_type());
-  float dbs[NGB];
+  float dbs[NGB];  // TR: row_sums gave both lane halves the whole tile's sum
 #pragma unroll
-  for (int gb = 0; gb < NGB; ++gb) dbs[gb] = pair_sum(dbacc[gb]) * inv_tau;
+  for (int gb = 0; gb < NGB; ++gb) dbs[gb] = (TR ? dbacc[gb] : pair_sum(dbacc[gb])) * inv_tau;
   const float dt = -kLn2 * inv_tau * half_wave_sum(dtacc);
   const int64_t E = part_floats_slice_bwd(G, D);
   float* pw = a.part + ((int64_t)bh * gridDim.x + blockIdx.x) * E;
@@ -504,7 +544,17 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
 // ---------------------------------------------------------------- deslice bwd
 template <typename T, int DK, int NGB, int NDB, int NVB>
 __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_deslice_bwd(Args a) {
-  FS_PROLOGUE(NGB, NDB, NVB, NGB * NVB + NDB * NGB)
+  // TR ((1,1,1), C2): the transposed operands (d_out^T, w^T, x^T, Lb^T) are
+  // the pieces already split for omega, the logits and dx, read back
+  // transposed (tr_put / tr_get), and db is their row sum on the matrix
+  // cores: 4 bf16x6 splits per tile instead of 7, no fp32 transposes. Each
+  // wave's LDS region holds x's pieces and one region that carries d_out's,
+  // then w's, then Lb's.
+  constexpr bool TR = NGB == 1 && NDB == 1 && NVB == 1;
+  FS_PROLOGUE(NGB, NDB, NVB, NGB * NVB + NDB * NGB, TR ? tr_wave_floats<DK>() : kLdsTile)
+  char* trX = reinterpret_cast<char*>(lds);
+  char* trS = trX + tr_bytes<ML>();
+  (void)trS;
   // tokens as [g-outer, v-inner] (omega, qTr[gb * NVB + vb]); W as [d-outer,
   // g-inner] (dx).
   u32x4* qTr = qV;
@@ -557,6 +607,7 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
         Frag<ML> xq[NDB];
 #pragma unroll
         for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xf[db]);
+        if constexpr (TR) tr_put<ML>(trX, xq[0], c, h, 0u);
         FS_LOGITS(t2, xq)
       }
       // everything d_out feeds is prepared before the softmax (omega, and
@@ -567,6 +618,7 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
         Frag<MV> oq[NVB];
 #pragma unroll
         for (int vb = 0; vb < NVB; ++vb) prep<MV>(oq[vb], of[vb]);
+        if constexpr (TR) tr_put<MV>(trS, oq[0], c, h, 0u);
 #pragma unroll
         for (int gb = 0; gb < NGB; ++gb) {
           f32x16 o = zero16();
@@ -579,43 +631,61 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
           from16(om[gb], o);
         }
       }
-      // d_out^T, carrying the tile's sign (acc_add); split into MFMA pieces
-      // here when several slot blocks share it, else next to its one use
-      // (16 registers across the softmax instead of the split's 24)
-      float oT[NVB][16];
-      Frag<MV> oTq[NVB];
+      if constexpr (TR) {
+        load_g(t + a.P);
+        softmax_tile<NGB>(w, m2, lsum, t2, pv);
+        // dtokens += w^T d_out: d_out^T from its pieces; w (carrying the
+        // tile's sign, acc_add) split and read back transposed
+        Frag<MV> oTq, wq, wTq;
+        tr_get<MV>(oTq, trS, lane);
+        float ws[16];
 #pragma unroll
-      for (int vb = 0; vb < NVB; ++vb) {
-        transpose32(oT[vb], of[vb], lds, c, h);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) oT[vb][j] *= sg;
-        if constexpr (NGB > 1) prep<MV>(oTq[vb], oT[vb]);
-      }
-      load_g(t + a.P);
-      softmax_tile<NGB>(w, m2, lsum, t2, pv);
-      // dtokens += w^T d_out (rows of d_out beyond N read as zero)
-#pragma unroll
-      for (int gb = 0; gb < NGB; ++gb) {
-        float wT[16];
-        transpose32(wT, w[gb], lds, c, h);
-        Frag<MV> wTq;
-        prep<MV>(wTq, wT);
+        for (int j = 0; j < 16; ++j) ws[j] = w[0][j] * sg;
+        prep<MV>(wq, ws);
+        tr_put<MV>(trS, wq, c, h, 0u);
+        tr_get<MV>(wTq, trS, lane);
+        mma_acc<MV>(dT[0][0], oTq, wTq, sg);
+        dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
+        FS_DX_DW_TR(om, qWc, sg)
+      } else {
+        // d_out^T, carrying the tile's sign (acc_add); split into MFMA pieces
+        // here when several slot blocks share it, else next to its one use
+        // (16 registers across the softmax instead of the split's 24)
+        float oT[NVB][16];
+        Frag<MV> oTq[NVB];
 #pragma unroll
         for (int vb = 0; vb < NVB; ++vb) {
-          if constexpr (NGB == 1) prep<MV>(oTq[vb], oT[vb]);
-          mma_acc<MV>(dT[gb][vb], oTq[vb], wTq, sg);
+          transpose32(oT[vb], of[vb], lds, c, h);
+#pragma unroll
+          for (int j = 0; j < 16; ++j) oT[vb][j] *= sg;
+          if constexpr (NGB > 1) prep<MV>(oTq[vb], oT[vb]);
         }
+        load_g(t + a.P);
+        softmax_tile<NGB>(w, m2, lsum, t2, pv);
+        // dtokens += w^T d_out (rows of d_out beyond N read as zero)
+#pragma unroll
+        for (int gb = 0; gb < NGB; ++gb) {
+          float wT[16];
+          transpose32(wT, w[gb], lds, c, h);
+          Frag<MV> wTq;
+          prep<MV>(wTq, wT);
+#pragma unroll
+          for (int vb = 0; vb < NVB; ++vb) {
+            if constexpr (NGB == 1) prep<MV>(oTq[vb], oT[vb]);
+            mma_acc<MV>(dT[gb][vb], oTq[vb], wTq, sg);
+          }
+        }
+        dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
+        FS_DX_DW(om, qWc, sg)
       }
-      dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
-      FS_DX_DW(om, qWc, sg)
     };
     load_g(pid);
     FS_TILE_LOOP(load, body, xA, xB)
   };
   if (fast) run(std::true_type()); else run(std::false_type());
-  float dbs[NGB];
+  float dbs[NGB];  // TR: row_sums gave both lane halves the whole tile's sum
 #pragma unroll
-  for (int gb = 0; gb < NGB; ++gb) dbs[gb] = pair_sum(dbacc[gb]) * inv_tau;
+  for (int gb = 0; gb < NGB; ++gb) dbs[gb] = (TR ? dbacc[gb] : pair_sum(dbacc[gb])) * inv_tau;
   const float dt = -kLn2 * inv_tau * half_wave_sum(dtacc);
   const int64_t offW = (int64_t)G * DV, E = part_floats_deslice_bwd(G, D, DV);
   float* pw = a.part + ((int64_t)bh * gridDim.x + blockIdx.x) * E;

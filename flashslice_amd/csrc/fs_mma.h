@@ -159,6 +159,86 @@ __device__ __forceinline__ void mma_acc(f32x16& acc, const Frag<M>& a, const Fra
   acc_add(acc, mma<M>(a, b, zero16()), sgn);
 }
 
+// ------------------------------------------------ transposing split fragments
+// A fragment's bf16 pieces can be transposed through LDS without splitting
+// the transposed values again: the wave writes them as rows (tr_put) and
+// reads them back with ds_read_b64_tr_b16 (tr_get), gfx950's transposing LDS
+// load. Its lane layout, measured on the part: in each group of 16 lanes,
+// element i of lane q is element q % 4 of the 8 bytes that lane 4 i + q / 4
+// of the group addressed. So if lane (group g, index L) of the reading wave
+// addresses row 16 s + 4 (g / 2) + L / 4 (+ 8), columns 16 (g % 2) + 4 (L % 4)
+// .. + 3, lane (c, h) receives column c of rows 16 s + 4 h + i (+ 8): the
+// transposed fragment in the MFMA operand layout (fragment convention of
+// fs_device.h).
+// Region of one fragment: [piece][32 rows][32 columns] bf16, rows of 64
+// bytes; the 8-byte column segments of a row are XOR-swizzled by the row's
+// group of four, so that both the row writes (lanes = rows) and the
+// transposing reads (4 rows x 16 columns per lane group) hit 64 distinct
+// banks per 256 bytes.
+constexpr int kTrRowB = 64, kTrPieceB = 32 * kTrRowB;
+template <int M> constexpr int tr_pieces() { return M == MMA_X6 ? 3 : 1; }
+template <int M> constexpr int tr_bytes() { return tr_pieces<M>() * kTrPieceB; }
+__device__ __forceinline__ int tr_off(int row, int col) {
+  return row * kTrRowB + ((col ^ (4 * ((row >> 2) & 7))) << 1);
+}
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4* LdsI16x4;
+
+// Write fragment f ([outer = c][inner = kmap(j, h)]) of lane (c, h) as rows;
+// `neg` (0 or 0x80008000) flips the sign of every piece written.
+template <int M>
+__device__ __forceinline__ void tr_put(char* region, const Frag<M>& f, int c, int h, uint32_t neg) {
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int pi = 0; pi < tr_pieces<M>(); ++pi)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const u32x4 w = f.q[2 * pi + s];
+      char* base = region + pi * kTrPieceB;
+      *reinterpret_cast<uint2*>(base + tr_off(c, 16 * s + 4 * h)) = make_uint2(w[0] ^ neg, w[1] ^ neg);
+      *reinterpret_cast<uint2*>(base + tr_off(c, 16 * s + 8 + 4 * h)) =
+          make_uint2(w[2] ^ neg, w[3] ^ neg);
+    }
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Read the transposed fragment ([outer = column][inner = kmap(j, h) over
+// rows]) of what tr_put wrote (pieces of mode M, M's own piece count: an
+// MMA_BF16 read of MMA_X6 pieces takes piece 0, the bf16 rounding).
+template <int M>
+__device__ __forceinline__ void tr_get(Frag<M>& f, const char* region, int lane) {
+  const int L = lane & 15, g = lane >> 4;
+  const int r0 = 4 * (g >> 1) + (L >> 2), col = 16 * (g & 1) + 4 * (L & 3);
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int pi = 0; pi < tr_pieces<M>(); ++pi)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const char* base = region + pi * kTrPieceB;
+      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (LdsI16x4)(const_cast<char*>(base) + tr_off(16 * s + r0, col)));
+      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (LdsI16x4)(const_cast<char*>(base) + tr_off(16 * s + 8 + r0, col)));
+      const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+      f.q[2 * pi + s] = u32x4{l2.x, l2.y, h2.x, h2.y};
+    }
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Row sums of a fragment B ([outer = c][inner = k]): sum_k B[c][k] in every
+// register of lane (c, h) (a ones operand times B on the bf16 matrix cores,
+// the result's lanes indexing B's outer axis; the pieces of an MMA_X6
+// fragment are exact, smallest first).
+template <int M> __device__ __forceinline__ f32x16 row_sums(const Frag<M>& b) {
+  const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  f32x16 t = zero16();
+#pragma unroll
+  for (int pi = tr_pieces<M>() - 1; pi >= 0; --pi)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) t = mfma_bf16(ones, b.q[2 * pi + s], t);
+  return t;
+}
+
 // Ready fragments in LDS: word w of lane l at slot[w * 64 + l] (16-byte
 // words; a wave reads or writes 1 KB of consecutive words per instruction,
 // conflict-free).
