@@ -72,9 +72,9 @@ class Case:
             B, G, H, D = self.B, self.G, self.H, self.D
             w = (L["t"] @ L["Wk"]).view(B, G, H, D).permute(0, 2, 1, 3)
             b = (L["t"] @ L["Wb"]).permute(0, 2, 1) if self.bias else None
-        if amp:
-            x, fx, w = x.bfloat16(), fx.bfloat16(), w.bfloat16()
-            b = None if b is None else b.bfloat16()
+        if amp:  # a 16-bit dtype: x, fx, W, b as the activations of an autocast region
+            x, fx, w = x.to(amp), fx.to(amp), w.to(amp)
+            b = None if b is None else b.to(amp)
         return x, fx, w, b, tau, tok
 
     def run(self, dtype, fused, device="cpu", amp=False, order="slice-first", grads=True):
@@ -107,12 +107,16 @@ class Case:
 
 
 def check_case(case, order="slice-first", dot="", kernel_mode="auto", gate=1.25,
-               blocked=False, grads=True, strict=True, ref_device="cpu"):
+               blocked=False, grads=True, strict=True, ref_device="cpu", inputs=None):
     """Run ``case`` through the oracle (fp64, fp32) and the HIP path twice;
     return a list of failure strings (empty = pass) and the metrics.
     ``ref_device``: where the oracle's tensors live (the full-size cases
-    evaluate the same restatement on the GPU's ATen kernels)."""
-    amp = dot in ("bf16", "bf16v")
+    evaluate the same restatement on the GPU's ATen kernels). ``inputs``:
+    None, "bf16" or "fp16" -- the point tensors and W, b in that dtype (the
+    bf16 dot levels imply bf16), eager upcasting them to fp32."""
+    amp = {"bf16": torch.bfloat16, "fp16": torch.float16}.get(inputs, False)
+    if dot in ("bf16", "bf16v"):
+        amp = torch.bfloat16
     ref = case.run(torch.float64, fused=False, device=ref_device, order=order, grads=grads)
     ea = case.run(torch.float32, fused=False, device=ref_device, amp=amp, order=order,
                   grads=grads)
@@ -130,9 +134,9 @@ def check_case(case, order="slice-first", dot="", kernel_mode="auto", gate=1.25,
         if k not in fu:
             fails.append("%s missing from the fused run" % k)
             continue
-        # under the bf16 dot modes the activations are bf16, so out (x_mid's
-        # dtype) is bf16 where the fp32-upcast eager run's is fp32
-        want_dtype = torch.bfloat16 if (amp and k == "out") else ea[k].dtype
+        # with 16-bit activations out (x_mid's dtype) is 16-bit where the
+        # fp32-upcast eager run's is fp32
+        want_dtype = amp if (amp and k == "out") else ea[k].dtype
         if fu[k].shape != ea[k].shape or fu[k].dtype != want_dtype:
             fails.append("%s: shape/dtype %s %s vs eager %s %s" % (
                 k, tuple(fu[k].shape), fu[k].dtype, tuple(ea[k].shape), ea[k].dtype))

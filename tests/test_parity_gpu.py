@@ -65,6 +65,39 @@ def test_bf16_dot_modes(dot):
             assert ef < 2e-2, (k, ef)
 
 
+@pytest.mark.parametrize("inputs", ["bf16", "fp16"])
+@pytest.mark.parametrize("G", [32, 256], ids=["whole-g", "g-blocked"])
+def test_half_point_tensors(inputs, G):
+    """16-bit x_mid, fx_mid, W and b with the default (fp32-accurate) dots:
+    the reference's bf16-autocast case (bench/parity_test.py:130-138), fwd
+    and bwd. out, dx and dfx come back in the input dtype; every output and
+    gradient within 2x of eager fp32 run on the same 16-bit inputs (errors of
+    the bf16 class; the reference's forward gate is 1.5x + 1e-3)."""
+    case = Case(B=1, N=2049, H=4, D=32, G=G, mode="hgd")
+    fails, rows = check_case(case, inputs=inputs, blocked=G > 128)
+    _report("%s-inputs-g%d" % (inputs, G), fails, rows)
+    for k, ee, ef, fe in rows:
+        assert ef < 0.05, (k, ef)
+
+
+@pytest.mark.parametrize("dot,kw,kmode", [
+    ("tf32", dict(B=1, N=4097, H=8, D=32, G=32, mode="hgd"), "auto"),
+    ("tf32", dict(B=1, N=2049, H=4, D=32, G=256, mode="hgd"), "blocked"),
+    ("tf32x3", dict(B=1, N=4097, H=8, D=32, G=32, mode="hgd"), "auto"),
+    ("tf32x3", dict(B=1, N=2049, H=2, D=32, G=128, mode="hgd"), "auto"),
+    ("tf32x3", dict(B=1, N=2049, H=4, D=32, G=256, mode="hgd"), "blocked"),
+], ids=["tf32", "blk-tf32-g256", "tf32x3", "tf32x3-g128", "blk-tf32x3-g256"])
+def test_tf32_levels(dot, kw, kmode):
+    """The opt-in tf32 levels (reference bench/parity_test.py:230-245, gate
+    10x). gfx950 has no tf32 MFMA: both run the fp32-accurate split, so they
+    also meet the ieee gates."""
+    fails, rows = check_case(Case(**kw), dot=dot, kernel_mode=kmode, gate=10.0,
+                             blocked=kmode == "blocked")
+    _report(dot, fails, rows)
+    strict, _ = check_case(Case(**kw), dot=dot, kernel_mode=kmode, blocked=kmode == "blocked")
+    assert not strict, strict
+
+
 def test_forced_blocked_mode_small_g():
     """kernel mode 'blocked' routes through the stats-carrying ops."""
     fails, rows = check_case(Case(B=1, N=2049, H=4, D=32, G=32, mode="bhgd"),
