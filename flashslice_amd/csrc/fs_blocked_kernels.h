@@ -602,7 +602,9 @@ __global__ __launch_bounds__(256, 2) void k_blk_bwd_g(Args a) {
 }
 
 // ---------------------------------------------------------------- launching
-// NB: 32-wide blocks held per point row for D and DV together (1, 2, 4, 8).
+// NB: 32-wide blocks held per point row for D and DV together. One or two
+// (D, DV <= 64) go to the prepared-fragment kernels of fs_gp_kernels.h; the
+// kernels of this file serve four and eight.
 template <int K, typename T, int DK>
 hipError_t blocked_launch(const Args& a, hipStream_t st) {
   const int nb = a.nd > a.nv ? a.nd : a.nv;
@@ -658,7 +660,7 @@ hipError_t blocked_launch(const Args& a, hipStream_t st) {
       hipLaunchKernelGGL((k_blk_bwd_g<T, DK, NB_, false>), gg, blk, 0, st, a);                 \
     return hipGetLastError();                                                                  \
   }
-  BK_TRY(1) BK_TRY(2) BK_TRY(4) BK_TRY(8)
+  BK_TRY(4) BK_TRY(8)
 #undef BK_TRY
   return hipErrorNotSupported;
 }

@@ -145,6 +145,8 @@ BLOCKED = [
     ("blk-g48-masked", dict(B=1, N=1537, H=4, D=32, G=48, mode="hgd"), "slice-first", "blocked"),
     ("blk-g8-padded", dict(B=1, N=1537, H=4, D=32, G=8, mode="hgd"), "slice-first", "blocked"),
     ("blk-d256-g32", dict(B=1, N=1025, H=2, D=256, G=32, mode="hgd"), "slice-first", "auto"),
+    ("blk-d128-g64-forced", dict(B=1, N=1537, H=2, D=128, DV=96, G=64, mode="hgd"),
+     "deslice-first", "blocked"),
     ("blk-d24-g40-dv24", dict(B=1, N=1537, H=4, D=24, DV=24, G=40, mode="hgd"),
      "deslice-first", "blocked"),
     ("blk-g1", dict(B=1, N=1025, H=2, D=56, DV=32, G=1, mode="bhgd", bias=False),
