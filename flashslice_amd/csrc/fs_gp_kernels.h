@@ -40,6 +40,9 @@ namespace fs {
 // one (512 registers) for two.
 constexpr int gp_waves(int nb) { return nb == 1 ? 2 : 1; }
 
+// Column blocks k < NB are guarded by the call's block counts nd / nv; block 0
+// always exists (D, DV >= 1), and saying so (k == 0 || k < nd) lets the MFMA
+// chains start without materialising a zero accumulator for the skipped case.
 template <int DK> struct GModes {
   static constexpr int L = (DK == 2) ? MMA_BF16 : MMA_X6;
   static constexpr int V = (DK >= 1) ? MMA_BF16 : MMA_X6;
@@ -188,7 +191,7 @@ __device__ __forceinline__ void gp_logits(float (&t2)[16], const u32x4* sw, cons
   f32x16 s = zero16();
 #pragma unroll
   for (int k = 0; k < NB; ++k)
-    if (k < nd) {
+    if (k == 0 || k < nd) {
       Frag<ML> wq;
       lds_get<ML>(wq, sw + k * frag_words<ML>(), lane);
       s = mma<ML>(wq, xq[k], s);
@@ -364,7 +367,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_deslice(Args a) {
       prep<MV>(eq, e);
 #pragma unroll
       for (int k = 0; k < NB; ++k)
-        if (k < nv) {
+        if (k == 0 || k < nv) {
           Frag<MV> tq;
           lds_get<MV>(tq, sw + NB * FWL + k * FWV, lane);
           acc[k] = mma<MV>(eq, tq, acc[k]);
@@ -378,7 +381,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_deslice(Args a) {
     const Rsrc ro = rows_rsrc(o_b, o_sn, o_w, p0, N);
 #pragma unroll
     for (int k = 0; k < NB; ++k)
-      if (k < nv) {
+      if (k == 0 || k < nv) {
         f32x16 o = acc[k];
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[r] *= inv_r[r];
@@ -448,7 +451,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_slice_g(Args a) {
       prep<MV>(wq, wT);
 #pragma unroll
       for (int k = 0; k < NB; ++k)
-        if (k < nv) {
+        if (k == 0 || k < nv) {
           Frag<MV> fq;
           prep<MV>(fq, fT[k]);
           mma_acc<MV>(zacc[k], fq, wq, sg);
@@ -467,7 +470,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_slice_g(Args a) {
   if (gg < G) {
 #pragma unroll
     for (int k = 0; k < NB; ++k)
-      if (k < nv)
+      if (k == 0 || k < nv)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int v = 32 * k + kmap(r, h);
@@ -551,91 +554,100 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_bwd_n(Args a) {
 #pragma unroll
     for (int k = 0; k < NB; ++k) acc[k] = zero16();
     float sdw = 0.f, lown = 0.f, delta = 0.f, inv_l = 0.f, rt = 0.f;
-    for (int s = 0; s < nstage; ++s, ++g) {
+    // one slot block: prefetch the next stage's fragments, logits, exponentials
+    // and omega of this one
+    auto stage_in = [&](int s, const u32x4*& sw, float (&t2)[16], float (&e)[16],
+                        float (&om)[16]) {
       if (s + 1 < nstage || more) stage((g + 1) & 1, (s + 1) % nstage);
-      const u32x4* sw = sbuf[g & 1];
-      float t2[16], e[16], om[16];
+      sw = sbuf[g & 1];
       gp_logits<ML, NB>(t2, sw, sw + O_BC, xq, nd, cst, lane);
 #pragma unroll
       for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(t2[r] - m2);
-      {
-        f32x16 o = zero16();
+      f32x16 o = zero16();
+#pragma unroll
+      for (int k = 0; k < NB; ++k)
+        if (k == 0 || k < nv) {
+          Frag<MV> vq;
+          lds_get<MV>(vq, sw + O_VR + k * FWV, lane);
+          o = mma<MV>(vq, fq[k], o);
+        }
+      float dsv[16];
+      if (SLICE) gp_vec(dsv, sw + O_DS, lane);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) om[r] = SLICE ? o[r] + dsv[r] : o[r];
+    };
+    // pass 1 over the slot blocks: row sum, delta numerator (and dfx)
+    for (int s = 0; s < ngb; ++s, ++g) {
+      const u32x4* sw;
+      float t2[16], e[16], om[16];
+      stage_in(s, sw, t2, e, om);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        lown += e[r];
+        sdw += e[r] * om[r];
+      }
+      if (SLICE) {
+        Frag<MV> eq;
+        prep<MV>(eq, e);
 #pragma unroll
         for (int k = 0; k < NB; ++k)
-          if (k < nv) {
-            Frag<MV> vq;
-            lds_get<MV>(vq, sw + O_VR + k * FWV, lane);
-            o = mma<MV>(vq, fq[k], o);
+          if (k == 0 || k < nv) {
+            Frag<MV> zq;
+            lds_get<MV>(zq, sw + O_X + k * FWV, lane);
+            acc[k] = mma<MV>(eq, zq, acc[k]);
           }
-        float dsv[16];
-        if (SLICE) gp_vec(dsv, sw + O_DS, lane);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) om[r] = SLICE ? o[r] + dsv[r] : o[r];
       }
-      if (s < ngb) {
-        // pass 1
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          lown += e[r];
-          sdw += e[r] * om[r];
-        }
-        if (SLICE) {
-          Frag<MV> eq;
-          prep<MV>(eq, e);
-#pragma unroll
-          for (int k = 0; k < NB; ++k)
-            if (k < nv) {
-              Frag<MV> zq;
-              lds_get<MV>(zq, sw + O_X + k * FWV, lane);
-              acc[k] = mma<MV>(eq, zq, acc[k]);
-            }
-        }
-        if (s == ngb - 1) {
-          const float l = pair_sum(lown);
-          inv_l = 1.f / l;
-          delta = pair_sum(sdw) * inv_l;
-          st_pt(pts_rsrc(sdel, p0, N), c, h, delta);
-          st_pt(pts_rsrc(slsum, p0, N), c, h, l);
-          if (SLICE) {
-            float inv_r[16];
-            gather_rows(inv_r, pv ? inv_l : 0.f, lds_x, c, h);
-            const Rsrc rdf = rows_rsrc(df_b, df_sn, df_w, p0, N);
-#pragma unroll
-            for (int k = 0; k < NB; ++k)
-              if (k < nv) {
-                f32x16 o = acc[k];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[r] *= inv_r[r];
-                st_cols<T>(rdf, vcf[k], (uint32_t)df_sn, o);
-              }
-          }
-#pragma unroll
-          for (int k = 0; k < NB; ++k) acc[k] = zero16();
-        }
-      } else {
-        // pass 2
-        float dl[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          dl[r] = (e[r] * om[r] - e[r] * delta) * inv_l;
-          rt = fmaf(dl[r], t2[r] - m2, rt);
-        }
-        Frag<MV> dq;
-        prep<MV>(dq, dl);
+      __syncthreads();
+    }
+    {
+      const float l = pair_sum(lown);
+      inv_l = 1.f / l;
+      delta = pair_sum(sdw) * inv_l;
+      st_pt(pts_rsrc(sdel, p0, N), c, h, delta);
+      st_pt(pts_rsrc(slsum, p0, N), c, h, l);
+      if (SLICE) {
+        float inv_r[16];
+        gather_rows(inv_r, pv ? inv_l : 0.f, lds_x, c, h);
+        const Rsrc rdf = rows_rsrc(df_b, df_sn, df_w, p0, N);
 #pragma unroll
         for (int k = 0; k < NB; ++k)
-          if (k < nd) {
-            Frag<MV> wq;
-            lds_get<MV>(wq, sw + O_X + k * FWV, lane);
-            acc[k] = mma<MV>(dq, wq, acc[k]);
+          if (k == 0 || k < nv) {
+            f32x16 o = acc[k];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[r] *= inv_r[r];
+            st_cols<T>(rdf, vcf[k], (uint32_t)df_sn, o);
           }
       }
+#pragma unroll
+      for (int k = 0; k < NB; ++k) acc[k] = zero16();
+    }
+    // pass 2: dl = (e omega - e delta) / l from the same rounded products,
+    // dx += dl (W / tau), the row term of dtau
+    for (int s = ngb; s < nstage; ++s, ++g) {
+      const u32x4* sw;
+      float t2[16], e[16], om[16];
+      stage_in(s, sw, t2, e, om);
+      float dl[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        dl[r] = (e[r] * om[r] - e[r] * delta) * inv_l;
+        rt = fmaf(dl[r], t2[r] - m2, rt);
+      }
+      Frag<MV> dq;
+      prep<MV>(dq, dl);
+#pragma unroll
+      for (int k = 0; k < NB; ++k)
+        if (k == 0 || k < nd) {
+          Frag<MV> wq;
+          lds_get<MV>(wq, sw + O_X + k * FWV, lane);
+          acc[k] = mma<MV>(dq, wq, acc[k]);
+        }
       __syncthreads();
     }
     const Rsrc rdx = rows_rsrc(dx_b, dx_sn, dx_w, p0, N);
 #pragma unroll
     for (int k = 0; k < NB; ++k)
-      if (k < nd) st_cols<T>(rdx, vcx[k], (uint32_t)dx_sn, acc[k]);
+      if (k == 0 || k < nd) st_cols<T>(rdx, vcx[k], (uint32_t)dx_sn, acc[k]);
     rt = pair_sum(rt);
     dtacc += (pv && h == 0) ? rt : 0.f;
   }
@@ -711,7 +723,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_bwd_g(Args a) {
         prep<MV>(wq, wT);
 #pragma unroll
         for (int k = 0; k < NB; ++k)
-          if (k < nv) {
+          if (k == 0 || k < nv) {
             float oT[16];
             transpose32(oT, ff[k], lds, c, h);
             Frag<MV> oq;
@@ -722,7 +734,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_bwd_g(Args a) {
       f32x16 o = zero16();
 #pragma unroll
       for (int k = 0; k < NB; ++k)
-        if (k < nv) {
+        if (k == 0 || k < nv) {
           Frag<MV> vq, fq;
           lds_get<MV>(vq, sq + O_VR + k * FWV, lane);
           prep<MV>(fq, ff[k]);
@@ -739,7 +751,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_bwd_g(Args a) {
       prep<MV>(aq, aT);
 #pragma unroll
       for (int k = 0; k < NB; ++k)
-        if (k < nd) {
+        if (k == 0 || k < nd) {
           float xT[16];
           transpose32(xT, xf[k], lds, c, h);
           Frag<MV> xtq;
@@ -761,7 +773,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_bwd_g(Args a) {
       float* pw = a.part + ((int64_t)bh * P + pid) * part_floats_slice_bwd(G, D);
 #pragma unroll
       for (int k = 0; k < NB; ++k)
-        if (k < nd)
+        if (k == 0 || k < nd)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int d = 32 * k + kmap(r, h);
@@ -773,13 +785,13 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_bwd_g(Args a) {
       const int64_t offW = (int64_t)G * DV, offB = offW + (int64_t)G * D;
 #pragma unroll
       for (int k = 0; k < NB; ++k) {
-        if (k < nv)
+        if (k == 0 || k < nv)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int v = 32 * k + kmap(r, h);
             if (v < DV) pw[(int64_t)gg * DV + v] = dT[k][r];
           }
-        if (k < nd)
+        if (k == 0 || k < nd)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int d = 32 * k + kmap(r, h);
