@@ -62,9 +62,31 @@ Geo geo_n(const fs_slice_params* p, int64_t target_blocks) {
 // partials per (b, h) of a whole-G launch: one per block of four waves
 int pb(const Geo& g) { return g.P / fs::kWavesPerBlock; }
 
-Geo geo_g(const fs_slice_params* p) {
+// Blocks per launch of the G-blocked kernels by kind, measured on MI355X at
+// C3 (N = 1e6, H = 8, D = DV = 32, G = 256 and 1024). The point-owned kernels
+// run best with several times more blocks than stay resident (the statistics
+// pass and the deslice most: 0.90 -> 0.68 ms for the deslice at G = 256 with
+// bf16 dots). The slot-owned ones want more with the bf16x6 split (their
+// 4096-block grids 6 % faster at G = 1024) and the fewest with bf16 dots
+// (dk 2: 512; 4096 was 15 % slower).
+enum GpGrid { GPG_STATS, GPG_DESLICE, GPG_BWD_N, GPG_SLOT };
+int64_t gp_blocks(GpGrid k, int dk) {
+  switch (k) {
+    case GPG_STATS: return 2048;
+    case GPG_DESLICE: return 4096;
+    case GPG_BWD_N: return 2048;
+    default: return dk == 2 ? 512 : 4096;
+  }
+}
+
+Geo geo_gp(const fs_slice_params* p, GpGrid k, int dk) { return geo_n(p, gp_blocks(k, dk)); }
+
+// slot-owned grids: the target is shared among the ceil(G / 32) slot blocks;
+// dk -1 sizes for the largest of the dot kinds (workspace planning)
+Geo geo_g(const fs_slice_params* p, int dk) {
   const int64_t nsg = (p->G + 31) / 32;
-  return geo_n(p, (512 + nsg - 1) / nsg);
+  const int64_t t = dk < 0 ? gp_blocks(GPG_SLOT, 0) : gp_blocks(GPG_SLOT, dk);
+  return geo_n(p, (t + nsg - 1) / nsg);
 }
 
 // Blocks per launch of the whole-G kernels (measured on MI355X at N = 1e6,
@@ -245,7 +267,7 @@ Workspace plan_ws(int32_t op, const fs_slice_params* p, char* base) {
     const Geo g = geo_n(p, fused_target(op));
     w.part = take((size_t)(bh * pb(g) * wave_floats(op, p)));
   } else {
-    const Geo gn = geo_n(p, 512), gg = geo_g(p);
+    const Geo gn = geo_gp(p, GPG_BWD_N, 0), gg = geo_g(p, -1);
     w.stats = take((size_t)(bh * 2 * p->N));
     if (op != FS_OP_SLICE_FWD) {
       w.delta = take((size_t)(bh * p->N));
@@ -298,7 +320,7 @@ int32_t gp_prepare(fs::Args& a, const fs_slice_params* p, const Workspace& ws, i
 // `prepared`: a call's Args whose fragments are already built
 int32_t run_stats(const fs_points* x, const fs_slice_params* p, float* stats, int two_pass,
                   const fs::Args& prepared, hipStream_t st, const char* who) {
-  const Geo g = geo_n(p, 512);
+  const Geo g = geo_gp(p, GPG_STATS, 0);
   fs::Args a = base_args(p, g);
   set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
   a.vec_x = vec_ok(x);
@@ -340,7 +362,7 @@ int32_t fs_compute_stats(const fs_points* x, const fs_slice_params* p, float* st
   rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
-  fs::Args a = base_args(p, geo_n(p, 512));
+  fs::Args a = base_args(p, geo_gp(p, GPG_STATS, 0));
   rc = gp_prepare(a, p, ws, mode_of(p->dot, x->dtype), st, who);
   if (rc) return rc;
   return run_stats(x, p, stats, two_pass ? 1 : 0, a, st, who);
@@ -378,7 +400,7 @@ int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     a.stats_out = stats_out;
     rc = hip_check(fs::launch_fused_slice_fwd(a, x->dtype, mode, st), who);
   } else {
-    g = geo_g(p);
+    g = geo_g(p, mode);
     fs::Args a = base_args(p, g);
     set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
     set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
@@ -435,7 +457,7 @@ int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float
     a.stats_out = stats_out;
     return hip_check(fs::launch_fused_deslice_fwd(a, x->dtype, mode, st), who);
   }
-  const Geo g = geo_n(p, 512);
+  const Geo g = geo_gp(p, GPG_DESLICE, mode);
   fs::Args a = base_args(p, g);
   set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
   set_out(out, &a.o1, &a.s1b, &a.s1n, &a.s1h);
@@ -499,7 +521,7 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     rs.seg[1] = seg(ws.part, wf, (int64_t)G * D, pb(g), G, Bb, Hb, dbias);
     rs.seg[2] = seg(ws.part, wf, (int64_t)G * D + G, pb(g), 1, 1, (int)p->H, dtau);
   } else {
-    const Geo gn = geo_n(p, 512), gg = geo_g(p);
+    const Geo gn = geo_gp(p, GPG_BWD_N, mode), gg = geo_g(p, mode);
     fs::Args a = base_args(p, gn);
     set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
     set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
@@ -584,7 +606,7 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
     rs.seg[3] = seg(ws.part, wf, offB + G, pb(g), 1, 1, (int)p->H, dtau);
   } else {
     const float* stats = stats_in;
-    const Geo gn = geo_n(p, 512), gg = geo_g(p);
+    const Geo gn = geo_gp(p, GPG_BWD_N, mode), gg = geo_g(p, mode);
     fs::Args a = base_args(p, gn);
     set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
     set_in(d_out, &a.f, &a.sfb, &a.sfn, &a.sfh);
