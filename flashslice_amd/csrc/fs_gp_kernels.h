@@ -37,7 +37,11 @@
 namespace fs {
 
 // Waves per SIMD the kernels are compiled for: two for one 32-column block,
-// one (512 registers) for two.
+// one (512 registers) for two. With one block, the slot-owned slice forward,
+// the point-owned backward and the slot-owned slice backward are compiled for
+// three (168 registers, a few values spilled): measured at C3 (G = 256),
+// 1-7 % faster each; the slot-owned deslice backward spills too much there
+// (288 bytes per lane, 29 % slower) and keeps two.
 constexpr int gp_waves(int nb) { return nb == 1 ? 2 : 1; }
 
 // Column blocks k < NB are guarded by the call's block counts nd / nv; block 0
@@ -393,9 +397,11 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_deslice(Args a) {
 
 // ------------------------------------------------------------------ slice (g)
 // One slot block per block (blockIdx.x, fastest), point partition
-// blockIdx.y, head blockIdx.z: z_num, s partials of its 32 slots.
+// blockIdx.y, head blockIdx.z: z_num, s partials of its 32 slots. Compiled
+// for three waves per SIMD with one column block (168 registers and a few
+// spilled values; measured 2 % faster at C3 than two waves with 192).
 template <typename T, int DK, int NB>
-__global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_slice_g(Args a) {
+__global__ __launch_bounds__(256, NB == 1 ? 3 : 1) void k_gp_slice_g(Args a) {
   constexpr int ML = GModes<DK>::L, MV = GModes<DK>::V;
   constexpr int FWL = frag_words<ML>();
   __shared__ __attribute__((aligned(16))) u32x4 sq[NB * FWL + kGpVecFw];
@@ -489,7 +495,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_slice_g(Args a) {
 // temperature gradient. delta and l go to the slot-owned pass.
 // SLICE: omega = fx . dz_num + ds, also writes dfx; else omega = d_out . T.
 template <typename T, int DK, int NB, bool SLICE>
-__global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_bwd_n(Args a) {
+__global__ __launch_bounds__(256, NB == 1 ? 3 : gp_waves(NB)) void k_gp_bwd_n(Args a) {
   constexpr int ML = GModes<DK>::L, MV = GModes<DK>::V;
   constexpr int FWL = frag_words<ML>(), FWV = frag_words<MV>();
   // stage layout: W (logits) | V rows (omega) | V cols (dfx, pass 1) or W / tau (dx, pass 2)
@@ -661,7 +667,7 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_bwd_n(Args a) {
 // SLICE: dW, db partials (omega = fx . dz_num + ds); else also dtokens
 // (omega = d_out . T).
 template <typename T, int DK, int NB, bool SLICE>
-__global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_bwd_g(Args a) {
+__global__ __launch_bounds__(256, NB == 1 && SLICE ? 3 : gp_waves(NB)) void k_gp_bwd_g(Args a) {
   constexpr int ML = GModes<DK>::L, MV = GModes<DK>::V;
   constexpr int FWL = frag_words<ML>(), FWV = frag_words<MV>();
   constexpr int O_VR = NB * FWL, O_BC = O_VR + NB * FWV, O_DS = O_BC + kGpVecFw;
