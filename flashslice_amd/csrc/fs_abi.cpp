@@ -89,15 +89,18 @@ Geo geo_g(const fs_slice_params* p, int dk) {
   return geo_n(p, (t + nsg - 1) / nsg);
 }
 
-// Blocks per launch of the whole-G kernels (measured on MI355X at N = 1e6,
-// H = 8, D = DV = G = 32): the kernels that write point rows run best with
-// about three times more blocks than stay resident (two waves per SIMD), so
-// that the hardware keeps refilling CUs as blocks finish.
-int64_t fused_target(int32_t op) {
+// Blocks per launch of the whole-G kernels (measured on MI355X at C2: N = 1e6,
+// H = 8, D = DV = G = 32, and at C4: G = 64, DV = 64): the kernels run best
+// with several times more blocks than stay resident, so that the hardware
+// keeps refilling CUs as blocks finish -- except the deslice backward, whose
+// blocks each stream long runs of tiles, and the slice forward of the wider
+// shapes (one wave per SIMD; C4 5 % slower at 1024 blocks than at 512).
+int64_t fused_target(int32_t op, const fs_slice_params* p) {
+  const bool one = p->G <= 32 && p->D <= 32 && p->DV <= 32;
   switch (op) {
-    case FS_OP_DESLICE_FWD: return 1536;
-    case FS_OP_SLICE_BWD: return 1536;
-    default: return 512;
+    case FS_OP_DESLICE_BWD: return 512;
+    case FS_OP_SLICE_FWD: return one ? 1536 : 512;
+    default: return 1536;
   }
 }
 
@@ -264,7 +267,7 @@ Workspace plan_ws(int32_t op, const fs_slice_params* p, char* base) {
   }
   if (family_of(p) == 1) {
     // whole-G kernels leave one partial per block (its four waves summed)
-    const Geo g = geo_n(p, fused_target(op));
+    const Geo g = geo_n(p, fused_target(op, p));
     w.part = take((size_t)(bh * pb(g) * wave_floats(op, p)));
   } else {
     const Geo gn = geo_gp(p, GPG_BWD_N, 0), gg = geo_g(p, -1);
@@ -389,7 +392,7 @@ int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_par
   if (family_of(p) == 1) {
     // the whole-G kernels form the statistics exactly in their one pass, so
     // handed-in statistics (of these very logits) are not needed
-    g = geo_n(p, fused_target(FS_OP_SLICE_FWD));
+    g = geo_n(p, fused_target(FS_OP_SLICE_FWD, p));
     fs::Args a = base_args(p, g);
     set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
     set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
@@ -446,7 +449,7 @@ int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float
   hipStream_t st = (hipStream_t)stream;
   const int mode = mode_of(p->dot, x->dtype);
   if (family_of(p) == 1) {
-    const Geo g = geo_n(p, fused_target(FS_OP_DESLICE_FWD));
+    const Geo g = geo_n(p, fused_target(FS_OP_DESLICE_FWD, p));
     fs::Args a = base_args(p, g);
     set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
     set_out(out, &a.o1, &a.s1b, &a.s1n, &a.s1h);
@@ -501,7 +504,7 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
   const int Bb = Bo_of(p->b_stride_b, p->B), Hb = Ho_of(p->b_stride_h, p->H);
   fs::ReduceSegments rs{};
   if (family_of(p) == 1) {
-    const Geo g = geo_n(p, fused_target(FS_OP_SLICE_BWD));
+    const Geo g = geo_n(p, fused_target(FS_OP_SLICE_BWD, p));
     fs::Args a = base_args(p, g);
     set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
     set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
@@ -587,7 +590,7 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
   const int Bb = Bo_of(p->b_stride_b, p->B), Hb = Ho_of(p->b_stride_h, p->H);
   fs::ReduceSegments rs{};
   if (family_of(p) == 1) {
-    const Geo g = geo_n(p, fused_target(FS_OP_DESLICE_BWD));
+    const Geo g = geo_n(p, fused_target(FS_OP_DESLICE_BWD, p));
     fs::Args a = base_args(p, g);
     set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
     set_in(d_out, &a.f, &a.sfb, &a.sfn, &a.sfh);
