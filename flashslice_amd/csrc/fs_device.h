@@ -106,6 +106,22 @@ __device__ __forceinline__ void mma32_acc(f32x16& acc, const float (&a)[16], con
   acc_add(acc, mma32<MODE>(a, b, zero16()), sgn);
 }
 
+// Scheduling hints for the machine scheduler (no instructions are emitted).
+// A tile's steps form short dependent chains (a split on the VALU, then an
+// MFMA chain on its pieces); left to itself the scheduler issues each MFMA
+// chain back to back, so one wave keeps only one of the two pipes busy.
+// sched_fence() closes a scheduling region; sched_mfma_valu<N, K>() asks for
+// the region's next N MFMAs to be issued one at a time, each followed by K
+// VALU instructions of the independent work placed in the same region.
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+template <int N, int K> __device__ __forceinline__ void sched_mfma_valu() {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, K, 0);
+  }
+}
+
 // ---------------------------------------------------------------- dtype I/O
 template <typename T> __device__ __forceinline__ float to_f(T v);
 template <> __device__ __forceinline__ float to_f<float>(float v) { return v; }

@@ -205,22 +205,30 @@ __global__ __launch_bounds__(256, NGB * NDB * NVB == 1 ? 3 : 1) void k_fused_sli
       const bool pv = p0 + c < N;
       constexpr float sg = decltype(par)::sign;
       float t2[NGB][16], w[NGB][16], m2, lsum;
+      Frag<MV> fq[NVB];  // fx carries the tile's sign (acc_add)
       {
         Frag<ML> xq[NDB];
 #pragma unroll
         for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xf[db]);
+        // one block on every axis: the logits on the matrix cores while fx
+        // is split (sched_mfma_valu)
+        constexpr bool IL = NGB * NDB * NVB == 1;
+        if constexpr (IL) sched_fence();
         FS_LOGITS(t2, xq)
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) {
+          float fs[16];
+#pragma unroll
+          for (int j = 0; j < 16; ++j) fs[j] = fT[vb][j] * sg;
+          prep<MV>(fq[vb], fs);
+        }
+        if constexpr (IL) {
+          sched_mfma_valu<12, 5>();
+          sched_fence();
+        }
       }
       softmax_tile<NGB>(w, m2, lsum, t2, pv);
       store_stats_tile(st_m, st_l, p0, N, c, h, m2, lsum);
-      Frag<MV> fq[NVB];  // fx carries the tile's sign (acc_add)
-#pragma unroll
-      for (int vb = 0; vb < NVB; ++vb) {
-        float fs[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) fs[j] = fT[vb][j] * sg;
-        prep<MV>(fq[vb], fs);
-      }
 #pragma unroll
       for (int gb = 0; gb < NGB; ++gb) {
         float wT[16];
@@ -376,7 +384,7 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
       Frag<MV> wc_;                                                                 \
       lds_get<MV>(wc_, QWC, lane);                                                  \
       const f32x16 o_ = mma<MV>(aq_, wc_, zero16());                                \
-      st_cols<T>(rows_rsrc(dx_b, dx_sn, dx_w, p0, N), vcx[0], (uint32_t)dx_sn, o_);  \
+      st_cols<T>(rows_rsrc_sel(dx_b, dx_sn, dx_w, p0, N), vcx[0], (uint32_t)dx_sn, o_);  \
     }                                                                               \
     tr_put<MV>(trS, aq_, c, h, (SG) < 0.f ? 0x80008000u : 0u);                      \
     Frag<MV> aTq_, xTq_;                                                            \
@@ -445,71 +453,114 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
     // buffer is reloaded for the wave's next tile right there
     float xA[NDB][16], xB[NDB][16], ff[NVB][16];
     auto load = [&](float (&xn)[NDB][16], int t) {
-      ld_rows<T, NDB, FAST>(xn, rows_rsrc(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
+      ld_rows<T, NDB, FAST>(xn, rows_rsrc_sel(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
     };
     auto load_f = [&](int t) {
-      ld_rows<T, NVB, FAST>(ff, rows_rsrc(f_b, f_sn, f_w, (int64_t)t * kTile, N), vrf, DV, h);
+      ld_rows<T, NVB, FAST>(ff, rows_rsrc_sel(f_b, f_sn, f_w, (int64_t)t * kTile, N), vrf, DV, h);
     };
     auto body = [&](const float (&xf)[NDB][16], int t, auto par) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
       constexpr float sg = decltype(par)::sign;
       float t2[NGB][16], w[NGB][16], m2, lsum;
-      {
-        Frag<ML> xq[NDB];
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xf[db]);
-        if constexpr (TR) tr_put<ML>(trX, xq[0], c, h, 0u);
-        FS_LOGITS(t2, xq)
-      }
-      // omega = fx . dz_num + ds (needs no weights: formed first, so that
-      // fx's buffer is reloaded for the next tile a whole tile ahead)
       float om[NGB][16];
-      {
-        Frag<MV> fq[NVB];
-#pragma unroll
-        for (int vb = 0; vb < NVB; ++vb) prep<MV>(fq[vb], ff[vb]);
-#pragma unroll
-        for (int gb = 0; gb < NGB; ++gb) {
-          f32x16 o = zero16();
-#pragma unroll
-          for (int vb = 0; vb < NVB; ++vb) {
-            Frag<MV> zq;
-            lds_get<MV>(zq, qZr + (gb * NVB + vb) * FWV, lane);
-            o = mma<MV>(zq, fq[vb], o);
-          }
-          float dsv[16];  // d s per output slot
-          lds_frag_vec(dsv, sDS + 32 * gb, h);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) om[gb][r] = o[r] + dsv[r];
-        }
-      }
-      load_f(t + a.P);
-      softmax_tile<NGB>(w, m2, lsum, t2, pv);
-      // dfx = w dz_num
-      {
-        f32x16 o[NVB];
-#pragma unroll
-        for (int vb = 0; vb < NVB; ++vb) o[vb] = zero16();
-#pragma unroll
-        for (int gb = 0; gb < NGB; ++gb) {
-          Frag<MV> wq;
-          prep<MV>(wq, w[gb]);
-#pragma unroll
-          for (int vb = 0; vb < NVB; ++vb) {
-            Frag<MV> zq;
-            lds_get<MV>(zq, qZc + (vb * NGB + gb) * FWV, lane);
-            o[vb] = mma<MV>(wq, zq, o[vb]);
-          }
-        }
-        const Rsrc rdf = rows_rsrc(df_b, df_sn, df_w, p0, N);
-#pragma unroll
-        for (int vb = 0; vb < NVB; ++vb) st_cols<T>(rdf, vcf[vb], (uint32_t)df_sn, o[vb]);
-      }
-      dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
       if constexpr (TR) {
+        // Three regions pair an MFMA chain with independent VALU work: the
+        // logits with fx's split, omega with the softmax, dfx with the
+        // Jacobian (sched_mfma_valu).
+        Frag<ML> xq[1];
+        prep<ML>(xq[0], xf[0]);
+        tr_put<ML>(trX, xq[0], c, h, 0u);
+        sched_fence();
+        FS_LOGITS(t2, xq)
+        Frag<MV> fq;
+        prep<MV>(fq, ff[0]);
+        sched_mfma_valu<12, 5>();
+        sched_fence();
+        // omega = fx . dz_num + ds; fx is dead once split, so its buffer is
+        // reloaded for the next tile a whole tile ahead
+        load_f(t + a.P);
+        sched_fence();
+        f32x16 o;
+        {
+          Frag<MV> zq;
+          lds_get<MV>(zq, qZr, lane);
+          o = mma<MV>(zq, fq, zero16());
+        }
+        softmax_tile<NGB>(w, m2, lsum, t2, pv);
+        sched_mfma_valu<12, 7>();
+        sched_fence();
+        {
+          float dsv[16];  // d s per output slot
+          lds_frag_vec(dsv, sDS, h);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) om[0][r] = o[r] + dsv[r];
+        }
+        // dfx = w dz_num
+        Frag<MV> wq;
+        prep<MV>(wq, w[0]);
+        sched_fence();
+        {
+          Frag<MV> zq;
+          lds_get<MV>(zq, qZc, lane);
+          const f32x16 df = mma<MV>(wq, zq, zero16());
+          st_cols<T>(rows_rsrc_sel(df_b, df_sn, df_w, p0, N), vcf[0], (uint32_t)df_sn, df);
+        }
+        dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
+        sched_mfma_valu<12, 6>();
+        sched_fence();
         FS_DX_DW_TR(om, qWc, sg)
       } else {
+        {
+          Frag<ML> xq[NDB];
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xf[db]);
+          FS_LOGITS(t2, xq)
+        }
+        // omega = fx . dz_num + ds (needs no weights: formed first, so that
+        // fx's buffer is reloaded for the next tile a whole tile ahead)
+        {
+          Frag<MV> fq[NVB];
+#pragma unroll
+          for (int vb = 0; vb < NVB; ++vb) prep<MV>(fq[vb], ff[vb]);
+#pragma unroll
+          for (int gb = 0; gb < NGB; ++gb) {
+            f32x16 o = zero16();
+#pragma unroll
+            for (int vb = 0; vb < NVB; ++vb) {
+              Frag<MV> zq;
+              lds_get<MV>(zq, qZr + (gb * NVB + vb) * FWV, lane);
+              o = mma<MV>(zq, fq[vb], o);
+            }
+            float dsv[16];  // d s per output slot
+            lds_frag_vec(dsv, sDS + 32 * gb, h);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) om[gb][r] = o[r] + dsv[r];
+          }
+        }
+        load_f(t + a.P);
+        softmax_tile<NGB>(w, m2, lsum, t2, pv);
+        // dfx = w dz_num
+        {
+          f32x16 o[NVB];
+#pragma unroll
+          for (int vb = 0; vb < NVB; ++vb) o[vb] = zero16();
+#pragma unroll
+          for (int gb = 0; gb < NGB; ++gb) {
+            Frag<MV> wq;
+            prep<MV>(wq, w[gb]);
+#pragma unroll
+            for (int vb = 0; vb < NVB; ++vb) {
+              Frag<MV> zq;
+              lds_get<MV>(zq, qZc + (vb * NGB + gb) * FWV, lane);
+              o[vb] = mma<MV>(wq, zq, o[vb]);
+            }
+          }
+          const Rsrc rdf = rows_rsrc_sel(df_b, df_sn, df_w, p0, N);
+#pragma unroll
+          for (int vb = 0; vb < NVB; ++vb) st_cols<T>(rdf, vcf[vb], (uint32_t)df_sn, o[vb]);
+        }
+        dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
         FS_DX_DW(om, qWc, sg)
       }
     };
@@ -594,47 +645,44 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
     // buffer is reloaded for the wave's next tile right there
     float xA[NDB][16], xB[NDB][16], of[NVB][16];
     auto load = [&](float (&xn)[NDB][16], int t) {
-      ld_rows<T, NDB, FAST>(xn, rows_rsrc(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
+      ld_rows<T, NDB, FAST>(xn, rows_rsrc_sel(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
     };
     auto load_g = [&](int t) {
-      ld_rows<T, NVB, FAST>(of, rows_rsrc(g_b, g_sn, g_w, (int64_t)t * kTile, N), vrg, DV, h);
+      ld_rows<T, NVB, FAST>(of, rows_rsrc_sel(g_b, g_sn, g_w, (int64_t)t * kTile, N), vrg, DV, h);
     };
     auto body = [&](const float (&xf)[NDB][16], int t, auto par) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
       constexpr float sg = decltype(par)::sign;
       float t2[NGB][16], w[NGB][16], m2, lsum;
-      {
-        Frag<ML> xq[NDB];
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xf[db]);
-        if constexpr (TR) tr_put<ML>(trX, xq[0], c, h, 0u);
-        FS_LOGITS(t2, xq)
-      }
-      // everything d_out feeds is prepared before the softmax (omega, and
-      // d_out transposed for dtokens), so that its buffer is reloaded for
-      // the next tile a whole tile ahead
       float om[NGB][16];
-      {
-        Frag<MV> oq[NVB];
-#pragma unroll
-        for (int vb = 0; vb < NVB; ++vb) prep<MV>(oq[vb], of[vb]);
-        if constexpr (TR) tr_put<MV>(trS, oq[0], c, h, 0u);
-#pragma unroll
-        for (int gb = 0; gb < NGB; ++gb) {
-          f32x16 o = zero16();
-#pragma unroll
-          for (int vb = 0; vb < NVB; ++vb) {
-            Frag<MV> tq;
-            lds_get<MV>(tq, qTr + (gb * NVB + vb) * FWV, lane);
-            o = mma<MV>(tq, oq[vb], o);
-          }
-          from16(om[gb], o);
-        }
-      }
       if constexpr (TR) {
+        // Three regions pair an MFMA chain with independent VALU work: the
+        // logits with d_out's split, omega with the softmax, dtokens with
+        // the Jacobian (sched_mfma_valu).
+        Frag<ML> xq[1];
+        prep<ML>(xq[0], xf[0]);
+        tr_put<ML>(trX, xq[0], c, h, 0u);
+        sched_fence();
+        FS_LOGITS(t2, xq)
+        Frag<MV> oq;
+        prep<MV>(oq, of[0]);
+        tr_put<MV>(trS, oq, c, h, 0u);
+        sched_mfma_valu<12, 5>();
+        sched_fence();
+        f32x16 o;
+        {
+          Frag<MV> tq;
+          lds_get<MV>(tq, qTr, lane);
+          o = mma<MV>(tq, oq, zero16());
+        }
+        // d_out is dead once split: its buffer is reloaded for the wave's
+        // next tile a whole tile ahead
         load_g(t + a.P);
         softmax_tile<NGB>(w, m2, lsum, t2, pv);
+        sched_mfma_valu<12, 7>();
+        sched_fence();
+        from16(om[0], o);
         // dtokens += w^T d_out: d_out^T from its pieces; w (carrying the
         // tile's sign, acc_add) split and read back transposed
         Frag<MV> oTq, wq, wTq;
@@ -645,39 +693,69 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
         prep<MV>(wq, ws);
         tr_put<MV>(trS, wq, c, h, 0u);
         tr_get<MV>(wTq, trS, lane);
+        sched_fence();
         mma_acc<MV>(dT[0][0], oTq, wTq, sg);
         dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
+        sched_mfma_valu<12, 6>();
+        sched_fence();
         FS_DX_DW_TR(om, qWc, sg)
       } else {
-        // d_out^T, carrying the tile's sign (acc_add); split into MFMA pieces
-        // here when several slot blocks share it, else next to its one use
-        // (16 registers across the softmax instead of the split's 24)
-        float oT[NVB][16];
-        Frag<MV> oTq[NVB];
+        {
+          Frag<ML> xq[NDB];
 #pragma unroll
-        for (int vb = 0; vb < NVB; ++vb) {
-          transpose32(oT[vb], of[vb], lds, c, h);
-#pragma unroll
-          for (int j = 0; j < 16; ++j) oT[vb][j] *= sg;
-          if constexpr (NGB > 1) prep<MV>(oTq[vb], oT[vb]);
+          for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xf[db]);
+          FS_LOGITS(t2, xq)
         }
-        load_g(t + a.P);
-        softmax_tile<NGB>(w, m2, lsum, t2, pv);
-        // dtokens += w^T d_out (rows of d_out beyond N read as zero)
+        // everything d_out feeds is prepared before the softmax (omega, and
+        // d_out transposed for dtokens), so that its buffer is reloaded for
+        // the next tile a whole tile ahead
+        {
+          Frag<MV> oq[NVB];
 #pragma unroll
-        for (int gb = 0; gb < NGB; ++gb) {
-          float wT[16];
-          transpose32(wT, w[gb], lds, c, h);
-          Frag<MV> wTq;
-          prep<MV>(wTq, wT);
+          for (int vb = 0; vb < NVB; ++vb) prep<MV>(oq[vb], of[vb]);
 #pragma unroll
-          for (int vb = 0; vb < NVB; ++vb) {
-            if constexpr (NGB == 1) prep<MV>(oTq[vb], oT[vb]);
-            mma_acc<MV>(dT[gb][vb], oTq[vb], wTq, sg);
+          for (int gb = 0; gb < NGB; ++gb) {
+            f32x16 o = zero16();
+#pragma unroll
+            for (int vb = 0; vb < NVB; ++vb) {
+              Frag<MV> tq;
+              lds_get<MV>(tq, qTr + (gb * NVB + vb) * FWV, lane);
+              o = mma<MV>(tq, oq[vb], o);
+            }
+            from16(om[gb], o);
           }
         }
-        dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
-        FS_DX_DW(om, qWc, sg)
+        {
+          // d_out^T, carrying the tile's sign (acc_add); split into MFMA pieces
+          // here when several slot blocks share it, else next to its one use
+          // (16 registers across the softmax instead of the split's 24)
+          float oT[NVB][16];
+          Frag<MV> oTq[NVB];
+#pragma unroll
+          for (int vb = 0; vb < NVB; ++vb) {
+            transpose32(oT[vb], of[vb], lds, c, h);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) oT[vb][j] *= sg;
+            if constexpr (NGB > 1) prep<MV>(oTq[vb], oT[vb]);
+          }
+          load_g(t + a.P);
+          softmax_tile<NGB>(w, m2, lsum, t2, pv);
+          // dtokens += w^T d_out (rows of d_out beyond N read as zero)
+#pragma unroll
+          for (int gb = 0; gb < NGB; ++gb) {
+            float wT[16];
+            transpose32(wT, w[gb], lds, c, h);
+            Frag<MV> wTq;
+            prep<MV>(wTq, wT);
+#pragma unroll
+            for (int vb = 0; vb < NVB; ++vb) {
+              if constexpr (NGB == 1) prep<MV>(oTq[vb], oT[vb]);
+              mma_acc<MV>(dT[gb][vb], oTq[vb], wTq, sg);
+            }
+          }
+          dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
+          FS_DX_DW(om, qWc, sg)
+        }
       }
     };
     load_g(pid);

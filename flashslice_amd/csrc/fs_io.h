@@ -42,6 +42,21 @@ __device__ __forceinline__ Rsrc rows_rsrc(const void* base, int64_t snb, int64_t
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(p), (short)0, (int)rem, kRsrcWord3);
 }
 
+// rows_rsrc formed with selects instead of a branch (the compiler branches
+// over the 64-bit multiply of the form above): one multiply of the start row
+// clamped to N. Used inside the tile bodies whose steps are interleaved by
+// scheduling hints, where a branch would end the scheduling region; the
+// branching form costs fewer registers where that matters more.
+__device__ __forceinline__ Rsrc rows_rsrc_sel(const void* base, int64_t snb, int64_t rowb,
+                                              int64_t p0, int64_t N) {
+  const bool in = p0 < N;
+  const int64_t off = (in ? p0 : N) * snb;
+  int64_t rem = (N - 1) * snb + rowb - off;
+  rem = !in ? 0 : rem > 0x7fffffff ? 0x7fffffff : rem;
+  const char* p = (const char*)base + (in ? off : 0);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(p), (short)0, (int)rem, kRsrcWord3);
+}
+
 // Typed single-element and four-element accesses (fp32 compute values).
 template <typename T> struct Buf;
 template <> struct Buf<float> {

@@ -171,15 +171,20 @@ __device__ __forceinline__ void mma_acc(f32x16& acc, const Frag<M>& a, const Fra
 // transposed fragment in the MFMA operand layout (fragment convention of
 // fs_device.h).
 // Region of one fragment: [piece][32 rows][32 columns] bf16, rows of 64
-// bytes; the 8-byte column segments of a row are XOR-swizzled by the row's
-// group of four, so that both the row writes (lanes = rows) and the
-// transposing reads (4 rows x 16 columns per lane group) hit 64 distinct
-// banks per 256 bytes.
+// bytes; the eight 8-byte column segments of a row are XOR-swizzled by
+// (row / 2) % 8. Measured on MI355X, 8-byte LDS writes are served 16 lanes
+// at a time against 32 banks of 4 bytes, 8-byte reads (plain and
+// transposing) 32 lanes at a time against 64 banks. A row write's 16 lanes
+// are 16 consecutive rows at one segment: rows of equal parity share their
+// banks modulo 32 and the swizzle gives the 8 of each parity 8 different
+// segments (a (row / 4) % 8 swizzle leaves pairs of them colliding: 30 %
+// slower writes). A transposing read's 32 lanes cover 4 whole rows,
+// conflict-free under any swizzle within rows.
 constexpr int kTrRowB = 64, kTrPieceB = 32 * kTrRowB;
 template <int M> constexpr int tr_pieces() { return M == MMA_X6 ? 3 : 1; }
 template <int M> constexpr int tr_bytes() { return tr_pieces<M>() * kTrPieceB; }
 __device__ __forceinline__ int tr_off(int row, int col) {
-  return row * kTrRowB + ((col ^ (4 * ((row >> 2) & 7))) << 1);
+  return row * kTrRowB + ((col ^ (4 * ((row >> 1) & 7))) << 1);
 }
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4* LdsI16x4;
