@@ -100,6 +100,7 @@ int64_t fused_target(int32_t op, const fs_slice_params* p) {
   switch (op) {
     case FS_OP_DESLICE_BWD: return 512;
     case FS_OP_SLICE_FWD: return one ? 1536 : 512;
+    case FS_OP_DESLICE_FWD: return one ? 2048 : 1536;
     default: return 1536;
   }
 }

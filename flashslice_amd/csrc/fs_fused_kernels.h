@@ -243,7 +243,7 @@ __global__ __launch_bounds__(256, NGB * NDB * NVB == 1 ? 3 : 1) void k_fused_sli
         sacc[gb] += s;
       }
     };
-    FS_TILE_LOOP(load, body, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
+    FS_TILE_LOOP(load, body, true, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
   };
   if (fast) run(std::true_type()); else run(std::false_type());
   float ssum[NGB];
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
 #pragma unroll
       for (int vb = 0; vb < NVB; ++vb) st_cols<T>(ro, vco[vb], (uint32_t)o_sn, o[vb]);
     };
-    FS_TILE_LOOP(load, body, xA, xB)
+    FS_TILE_LOOP(load, body, true, xA, xB)
   };
   if (fast) run(std::true_type()); else run(std::false_type());
 }
@@ -565,7 +565,7 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
       }
     };
     load_f(pid);
-    FS_TILE_LOOP(load, body, xA, xB)
+    FS_TILE_LOOP(load, body, true, xA, xB)
   };
   if (fast) run(std::true_type()); else run(std::false_type());
   float dbs[NGB];  // TR: row_sums gave both lane halves the whole tile's sum
@@ -759,7 +759,7 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
       }
     };
     load_g(pid);
-    FS_TILE_LOOP(load, body, xA, xB)
+    FS_TILE_LOOP(load, body, true, xA, xB)
   };
   if (fast) run(std::true_type()); else run(std::false_type());
   float dbs[NGB];  // TR: row_sums gave both lane halves the whole tile's sum

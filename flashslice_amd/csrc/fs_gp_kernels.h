@@ -467,7 +467,7 @@ __global__ __launch_bounds__(256, NB == 1 ? 3 : 1) void k_gp_slice_g(Args a) {
       for (int j = 0; j < 16; ++j) s += wT[j];
       sacc = fmaf(s, sg, sacc);
     };
-    FS_TILE_LOOP(load, body, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
+    FS_TILE_LOOP(load, body, false, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
   };
   if (fast) run(std::true_type()); else run(std::false_type());
   float* pw = a.part + ((int64_t)bh * P + pid) * part_floats_slice_fwd(G, DV);
@@ -813,7 +813,7 @@ __global__ __launch_bounds__(256, NB == 1 && SLICE ? 3 : gp_waves(NB)) void k_gp
       for (int j = 0; j < 16; ++j) s += aT[j];
       dbacc = fmaf(s, sg, dbacc);
     };
-    FS_TILE_LOOP(load, body, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
+    FS_TILE_LOOP(load, body, false, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
   };
   if (fast) run(std::true_type()); else run(std::false_type());
   const int gg = 32 * gb + c;

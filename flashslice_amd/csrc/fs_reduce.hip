@@ -47,10 +47,19 @@ __global__ __launch_bounds__(256) void k_reduce_segments(int B, int H, ReduceSeg
     return (double)part[((int64_t)(bb * H + hh) * P + pp) * wstride + sg.off + e];
   };
   // group grp sums contributors grp, grp + 8, ... into four accumulators
-  // (contributor grp + 8 j goes to accumulator j % 4), four loads in flight
+  // (contributor grp + 8 j goes to accumulator j % 4); sixteen loads are
+  // issued before their adds (the sum is latency-bound: a few dozen
+  // contributors per thread), the adds keep that order
   double acc[4] = {0.0, 0.0, 0.0, 0.0};
   if (e < sg.E) {
     int c = grp, j = 0;
+    for (; c + 8 * 15 < C; c += 8 * 16, j += 16) {
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = (float)load(c + 8 * u);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) acc[u & 3] += (double)v[u];
+    }
     for (; c + 24 < C; c += 32, j += 4) {
       const double v0 = load(c), v1 = load(c + 8), v2 = load(c + 16), v3 = load(c + 24);
       acc[0] += v0;

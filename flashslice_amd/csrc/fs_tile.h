@@ -214,6 +214,25 @@ __device__ __forceinline__ void copy_frags(float (&dst)[NB][16], const float (&s
     for (int j = 0; j < 16; ++j) dst[k][j] = src[k][j];
 }
 
+// Issue priority of a wave from its remaining tiles (after tile t of the
+// sequence pid, pid + P, ... below ntiles): the quarter of its work still
+// ahead of it, 3 (all of it) down to 0. Waves of one SIMD that share a
+// priority level issue oldest first, which on MI355X let the waves resident
+// together finish the same number of tiles up to 1.6x apart (per-block
+// timestamps), leaving a tail in which a fraction of the resident waves
+// streams alone; with the level falling as a wave gets ahead, the waves that
+// lag are served first and the resident waves finish close together
+// (FS_TILE_LOOP with BAL; measured faster for the whole-G kernels at C2,
+// neutral to slower for the G-blocked kernels, which do without it).
+__device__ __forceinline__ void balance_prio(int t, int pid, int ntiles, int P) {
+  const int left = (ntiles - 1 - t) / P, total = (ntiles - 1 - pid) / P + 1;
+  const int l4 = 4 * left;
+  if (l4 >= 3 * total) __builtin_amdgcn_s_setprio(3);
+  else if (l4 >= 2 * total) __builtin_amdgcn_s_setprio(2);
+  else if (l4 >= total) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
 // The tile loop of the point-streaming kernels (wave pid owns tiles pid,
 // pid + a.P, ...): two register sets of point
 // rows alternate, each reloaded (two tiles ahead) right after the tile it
@@ -222,7 +241,7 @@ __device__ __forceinline__ void copy_frags(float (&dst)[NB][16], const float (&s
 // outstanding as on every back edge: the compiler then waits only for the
 // rows a tile needs, never for the stores still in flight. A load beyond the
 // last tile reads an empty range (zeros, no memory traffic).
-#define FS_TILE_LOOP(LOAD, BODY, A_ARGS, B_ARGS)                                          \
+#define FS_TILE_LOOP(LOAD, BODY, BAL, A_ARGS, B_ARGS)                                     \
   {                                                                                       \
     int t_ = pid;                                                                         \
     LOAD(A_ARGS, t_);                                                                     \
@@ -230,14 +249,17 @@ __device__ __forceinline__ void copy_frags(float (&dst)[NB][16], const float (&s
     if (t_ < a.ntiles) {                                                                  \
       BODY(A_ARGS, t_, TileEven());                                                       \
       LOAD(A_ARGS, t_ + 2 * a.P);                                                         \
+      if constexpr (BAL) balance_prio(t_, pid, a.ntiles, a.P);                            \
       t_ += a.P;                                                                          \
       while (t_ < a.ntiles) {                                                             \
         BODY(B_ARGS, t_, TileOdd());                                                      \
         LOAD(B_ARGS, t_ + 2 * a.P);                                                       \
+        if constexpr (BAL) balance_prio(t_, pid, a.ntiles, a.P);                          \
         t_ += a.P;                                                                        \
         if (t_ >= a.ntiles) break;                                                        \
         BODY(A_ARGS, t_, TileEven());                                                     \
         LOAD(A_ARGS, t_ + 2 * a.P);                                                       \
+        if constexpr (BAL) balance_prio(t_, pid, a.ntiles, a.P);                          \
         t_ += a.P;                                                                        \
       }                                                                                   \
     }                                                                                     \
