@@ -353,8 +353,8 @@ __global__ __launch_bounds__(256, 2) void k_blk_slice_g(Args a) {
 // ---------------------------------------------------- slice / deslice bwd (n)
 // Point-owned backward (reference blocked.py:576-673, :744-815). Pass 1 over
 // the slot blocks: the Jacobian numerator sum_g e omega (and, for the slice,
-// dfx = e dz_num), divided by l once. Pass 2: dl = (e omega - e delta) / l
-// from the same rounded products, dx += dl W, and the row term
+// dfx = e dz_num), divided by l once. Pass 2: dl = e (omega - delta) / l (the
+// difference first, as in the G-blocked kernels), dx += dl W, and the row term
 // sum_g dl (t2 - m2) of the temperature gradient, formed row by row over
 // all of G before anything is added across rows.
 // SLICE: omega = fx . dz_num + ds, also writes dfx; else omega = d_out . T.
@@ -392,11 +392,13 @@ __global__ __launch_bounds__(256, 2) void k_blk_bwd_n(Args a) {
       blk_rowouter<NB>(wA, Wp, 32 * gb, G, D, nd, c, h);
       blk_bias(bc, Bp, 32 * gb, G, cst, h);
       blk_logits<ML, NB>(t2, wA, xf, bc, cst, nd);
+      float lb = 0.f;  // per slot block, then across blocks
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         e[r] = __builtin_amdgcn_exp2f(t2[r] - m2);
-        lown += e[r];
+        lb += e[r];
       }
+      lown += lb;
       if (SLICE) {
         float zc[NB][16];
         blk_colouter<NB>(zc, Zp, 32 * gb, G, DV, nv, c, h);
@@ -412,8 +414,10 @@ __global__ __launch_bounds__(256, 2) void k_blk_bwd_n(Args a) {
         if (k < nv) o = mma32<MV>(zr[k], ff[k], o);
       float dsv[16];
       if (SLICE) blk_vec(dsv, Sp, 32 * gb, G, h);
+      float sb = 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sdw += e[r] * (SLICE ? o[r] + dsv[r] : o[r]);
+      for (int r = 0; r < 16; ++r) sb = fmaf(e[r], SLICE ? o[r] + dsv[r] : o[r], sb);
+      sdw += sb;
     }
     sdw += xor32(sdw);
     const float l = lown + xor32(lown);
@@ -454,14 +458,15 @@ __global__ __launch_bounds__(256, 2) void k_blk_bwd_n(Args a) {
         if (k < nv) o = mma32<MV>(zr[k], ff[k], o);
       float dsv[16];
       if (SLICE) blk_vec(dsv, Sp, 32 * gb, G, h);
-      float dl[16];
+      float dl[16], rb = 0.f;  // row term per slot block, then across blocks
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float e = __builtin_amdgcn_exp2f(t2[r] - m2);
         const float om = SLICE ? o[r] + dsv[r] : o[r];
-        dl[r] = (e * om - e * delta) * inv_l;
-        rt = fmaf(dl[r], t2[r] - m2, rt);
+        dl[r] = e * (om - delta) * inv_l;
+        rb = fmaf(dl[r], t2[r] - m2, rb);
       }
+      rt += rb;
       float wc[NB][16];
       blk_colouter<NB>(wc, Wp, 32 * gb, G, D, nd, c, h);
 #pragma unroll

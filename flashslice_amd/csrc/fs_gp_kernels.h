@@ -490,9 +490,11 @@ __global__ __launch_bounds__(256, NB == 1 ? 3 : 1) void k_gp_slice_g(Args a) {
 // Point-owned backward (reference blocked.py:576-673, :744-815). Pass 1 over
 // the slot blocks: the Jacobian numerator sum_g e omega (and, for the slice,
 // dfx = e dz_num), divided by the row sum l formed from the same
-// exponentials. Pass 2: dl = (e omega - e delta) / l from the same rounded
-// products, dx += dl (W / tau), and the row term sum_g dl (t2 - m2) of the
-// temperature gradient. delta and l go to the slot-owned pass.
+// exponentials. Pass 2: dl = e (omega - delta) / l (the difference first:
+// with a near-uniform softmax omega sits close to delta, and e omega - e delta
+// would cancel most of two rounded products), dx += dl (W / tau), and the row
+// term sum_g dl (t2 - m2) of the temperature gradient. delta and l go to the
+// slot-owned pass.
 // SLICE: omega = fx . dz_num + ds, also writes dfx; else omega = d_out . T.
 template <typename T, int DK, int NB, bool SLICE>
 __global__ __launch_bounds__(256, NB == 1 ? 3 : gp_waves(NB)) void k_gp_bwd_n(Args a) {
@@ -587,11 +589,14 @@ __global__ __launch_bounds__(256, NB == 1 ? 3 : gp_waves(NB)) void k_gp_bwd_n(Ar
       const u32x4* sw;
       float t2[16], e[16], om[16];
       stage_in(s, sw, t2, e, om);
+      float lb = 0.f, sb = 0.f;  // per slot block, then across blocks
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        lown += e[r];
-        sdw += e[r] * om[r];
+        lb += e[r];
+        sb = fmaf(e[r], om[r], sb);
       }
+      lown += lb;
+      sdw += sb;
       if (SLICE) {
         Frag<MV> eq;
         prep<MV>(eq, e);
@@ -627,18 +632,22 @@ __global__ __launch_bounds__(256, NB == 1 ? 3 : gp_waves(NB)) void k_gp_bwd_n(Ar
 #pragma unroll
       for (int k = 0; k < NB; ++k) acc[k] = zero16();
     }
-    // pass 2: dl = (e omega - e delta) / l from the same rounded products,
-    // dx += dl (W / tau), the row term of dtau
+    // pass 2: dl = e (omega - delta) / l, dx += dl (W / tau), the row term
+    // of dtau
     for (int s = ngb; s < nstage; ++s, ++g) {
       const u32x4* sw;
       float t2[16], e[16], om[16];
       stage_in(s, sw, t2, e, om);
-      float dl[16];
+      // the row term summed per slot block, then across blocks: dtau is a
+      // strongly cancelling sum, and one chain over all of G (128 terms at
+      // G = 256) lost ~15x eager's accuracy on it
+      float dl[16], rb = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        dl[r] = (e[r] * om[r] - e[r] * delta) * inv_l;
-        rt = fmaf(dl[r], t2[r] - m2, rt);
+        dl[r] = e[r] * (om[r] - delta) * inv_l;
+        rb = fmaf(dl[r], t2[r] - m2, rb);
       }
+      rt += rb;
       Frag<MV> dq;
       prep<MV>(dq, dl);
 #pragma unroll

@@ -109,15 +109,18 @@ __device__ __forceinline__ float jacobian_tile(float (&om)[NGB][16], const float
 #pragma unroll
     for (int r = 0; r < 16; ++r) d += w[gb][r] * om[gb][r];
   d = pair_sum(d);
-  float rt = 0.f;
+  float rt = 0.f;  // per slot block, then across blocks (a cancelling sum)
 #pragma unroll
-  for (int gb = 0; gb < NGB; ++gb)
+  for (int gb = 0; gb < NGB; ++gb) {
+    float rb = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const float lb = w[gb][r] * (om[gb][r] - d);
-      rt = fmaf(lb, t2s[gb][r], rt);
+      rb = fmaf(lb, t2s[gb][r], rb);
       om[gb][r] = lb;
     }
+    rt += rb;
+  }
   rt = pair_sum(rt);
   return (pv && h == 0) ? rt : 0.f;
 }
