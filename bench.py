@@ -59,6 +59,14 @@ WORKLOADS = {
            "C4: deslice->slice fwd+bwd, B=4 N=262144 H=8 D=32 DV=64 G=64 fp32 ieee, "
            "per-sample W, given tokens"),
 }
+# model-level workload: the Transolver that calls the path
+# once per layer, forward + backward of an MSE loss; reported on its own line
+MODEL_WORKLOADS = {
+    "c5": dict(B=1, N=2_000_000, space_dim=3, fun_dim=1, out_dim=4, n_hidden=256, n_heads=8,
+               n_layers=8, slice_num=32,
+               desc="C5: Transolver fwd+bwd (MSE), B=1 N=2e6, n_hidden=256, 8 heads, 8 layers, "
+                    "G=32, fp32, use_fused_slice=True"),
+}
 # dot level per run (reference slice_ops.py:336-343): 0 ieee; 3 bf16 (bf16 inputs)
 DOTS = {"ieee": 0, "bf16": 3}
 
@@ -212,12 +220,133 @@ def cpu_baseline(B, N, H, D, DV, G, layout, order, budget_s=20.0):
     return B * n / ts[1], n, torch.get_num_threads()
 
 
+def model_inputs(cfg, N, device, seed=0):
+    """Coordinates uniform in the unit cube, per-point inputs and MSE targets
+    ~N(0, 1), generated on the CPU from one seed."""
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.rand(cfg["B"], N, cfg["space_dim"], generator=g)
+    f = torch.randn(cfg["B"], N, cfg["fun_dim"], generator=g)
+    y = torch.randn(cfg["B"], N, cfg["out_dim"], generator=g)
+    return pos.to(device), f.to(device), y.to(device)
+
+
+def model_flops(model, cfg, N):
+    """Algorithmic flops of one forward + backward: every Linear applied per
+    point (2 in out forward, 4 in out for dX and dW) and the path's own dots
+    per layer (alg_flops); token-level products (on G tokens) and elementwise
+    work are left out."""
+    import torch.nn as nn
+    token_level = ("to_q", "to_k", "to_v", "slice_down", "in_project_slice",
+                   "in_project_deslice")
+    per_point = sum(6 * m.in_features * m.out_features for n, m in model.named_modules()
+                    if isinstance(m, nn.Linear) and not n.split(".")[-1] in token_level)
+    H = cfg["n_heads"]
+    D = cfg["n_hidden"] // H
+    path = cfg["n_layers"] * sum(alg_flops(cfg["B"], N, H, D, D, cfg["slice_num"]).values())
+    return cfg["B"] * N * per_point + path
+
+
+def bench_model(a, cfg):
+    """The config-5 model step on the fused operators: warmup, a determinism
+    check (two steps, bitwise equal loss and gradients), peak memory, then K
+    timed steps; the CPU baseline is the same model on its eager route on a
+    bounded sample of points."""
+    from flashslice_amd.layers import Transolver
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    kw = {k: cfg[k] for k in ("space_dim", "fun_dim", "out_dim", "n_hidden", "n_heads",
+                              "n_layers", "slice_num")}
+    torch.manual_seed(0)
+    model = Transolver(use_fused_slice=True, **kw).to(dev)
+    assert model.use_fused_slice
+    B, N = cfg["B"], cfg["N"]
+    pos, f, y = model_inputs(cfg, N, dev)
+    print("[bench] %s" % cfg["desc"], file=sys.stderr, flush=True)
+
+    def step():
+        model.zero_grad(set_to_none=True)
+        loss = (model(pos, f) - y).square().mean()
+        loss.backward()
+        return loss.detach()
+
+    for _ in range(a.warmup):
+        step()
+    l1 = step()
+    g1 = [p.grad.clone() for p in model.parameters()]
+    l2 = step()
+    deterministic = bool(torch.equal(l1, l2) and all(
+        torch.equal(u, p.grad) for u, p in zip(g1, model.parameters())))
+    del g1
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    step()
+    torch.cuda.synchronize()
+    peak_gb = (torch.cuda.max_memory_allocated() - base) / 1e9
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(a.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e0, e1 in ev:
+        e0.record()
+        step()
+        e1.record()
+    torch.cuda.synchronize()
+    ms_step = 1e3 * (time.perf_counter() - t0) / a.steps
+    ms_ev = sum(e0.elapsed_time(e1) for e0, e1 in ev) / a.steps
+    flops = model_flops(model, cfg, N)
+    tf = flops / (ms_ev * 1e-3) / 1e12
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        torch.set_num_threads(os.cpu_count() or 1)
+        cmodel = Transolver(use_fused_slice=False, **kw)
+        cmodel.load_state_dict({k: v.cpu() for k, v in model.state_dict().items()})
+        n_s = 16384
+        cp, cf, cy = model_inputs(cfg, n_s, "cpu")
+
+        def cstep():
+            cmodel.zero_grad(set_to_none=True)
+            (cmodel(cp, cf) - cy).square().mean().backward()
+        cstep()
+        ts = []
+        for _ in range(3):
+            t = time.perf_counter()
+            cstep()
+            ts.append(time.perf_counter() - t)
+        ts.sort()
+        cpu = {"value": round(B * n_s / ts[1] / 1e6, 5), "unit": "Mpoints/s",
+               "cores": torch.get_num_threads(), "kind": "port",
+               "sample": "the same model (same weights) on its eager route, fp32 fwd+bwd of "
+                         "the MSE loss on %d of the %d points, median of 3 runs" % (n_s, N)}
+
+    line = {
+        "metric": "Transolver fwd+bwd Mpoints/s (config 5)",
+        "value": round(B * N / (ms_step * 1e-3) / 1e6, 3), "unit": "Mpoints/s",
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (random-init weights)",
+        "config": {"workload": cfg["desc"], **kw, "B": B, "N": N},
+        "roofline": {"bound": "mfma", "kernel": "whole step (hipBLASLt GEMMs + path)",
+                     "achieved": round(tf, 2), "peak": MFMA_PEAK_TFLOPS["ieee"],
+                     "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS["ieee"], 4),
+                     "traffic": None, "alg_flops": flops},
+        "peak_hbm_gb": round(peak_gb, 2),
+        "deterministic": deterministic,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default 50; 5 for the model workload)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps first (default 5; 2 for the model workload)")
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS) + sorted(MODEL_WORKLOADS))
     ap.add_argument("--dot", default="ieee", choices=sorted(DOTS),
                     help="dot level: ieee (fp32 inputs) or bf16 (x_mid, fx_mid, W in bf16)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -226,6 +355,9 @@ def main():
                          "a kernel of known traffic that calibrates rocprofv3's FETCH_SIZE / "
                          "WRITE_SIZE counters")
     a = ap.parse_args()
+    model = a.workload in MODEL_WORKLOADS
+    a.steps = (5 if model else 50) if a.steps is None else a.steps
+    a.warmup = (2 if model else 5) if a.warmup is None else a.warmup
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
         print("bench.py measures one GPU: every GPU box of this build has one, and the "
@@ -236,6 +368,8 @@ def main():
     import flashslice_amd.kernels  # noqa: F401  -- registers torch.ops.flashslice
     from flashslice_amd.kernels import _hip
 
+    if a.workload in MODEL_WORKLOADS:
+        return bench_model(a, MODEL_WORKLOADS[a.workload])
     B, N, H, D, DV, G, layout, order, desc = WORKLOADS[a.workload]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
