@@ -27,6 +27,7 @@ import torch
 import torch.nn as nn
 
 from ..kernels.slice_ops import fused_deslice, fused_slice, unsupported_dims
+from .basic import PointLinear
 
 logger = logging.getLogger(__name__)
 
@@ -73,8 +74,8 @@ class Physics_Attention_Irregular_Mesh(nn.Module):  # noqa: N801 (reference name
         self.softmax = nn.Softmax(dim=-1)
         self.dropout = nn.Dropout(dropout)
         self.temperature = nn.Parameter(torch.full((1, heads, 1, 1), 0.5))
-        self.in_project_x = nn.Linear(dim, inner)
-        self.in_project_fx = nn.Linear(dim, inner)
+        self.in_project_x = PointLinear(dim, inner)
+        self.in_project_fx = PointLinear(dim, inner)
         self.in_project_slice = nn.Linear(dim_head, slice_num)
         nn.init.orthogonal_(self.in_project_slice.weight)
         if untied_deslice:
@@ -86,7 +87,7 @@ class Physics_Attention_Irregular_Mesh(nn.Module):  # noqa: N801 (reference name
         self.to_k = nn.Linear(dim_head, sd, bias=False)
         self.to_v = nn.Linear(dim_head, sd, bias=False)
         self.slice_down = nn.Identity() if sd == dim_head else nn.Linear(sd, dim_head, bias=False)
-        self.to_out = nn.Sequential(nn.Linear(inner, dim), nn.Dropout(dropout))
+        self.to_out = nn.Sequential(PointLinear(inner, dim), nn.Dropout(dropout))
 
     # tokens (B, H, G, dim_head) -> mixed tokens (B, H, G, dim_head)
     def _mix_tokens(self, tokens):

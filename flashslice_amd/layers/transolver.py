@@ -21,7 +21,7 @@ import torch
 import torch.nn as nn
 from torch.nn.init import trunc_normal_
 
-from .basic import MLP
+from .basic import MLP, PointLinear
 from .physics_attention import TOKEN_EPS, Physics_Attention_Irregular_Mesh
 
 
@@ -48,7 +48,7 @@ class TransolverBlock(nn.Module):
                        act=act)
         if last_layer:
             self.ln_3 = nn.LayerNorm(hidden_dim)
-            self.mlp2 = nn.Linear(hidden_dim, out_dim)
+            self.mlp2 = PointLinear(hidden_dim, out_dim)
 
     def forward(self, fx, slice_weights_in=None):
         weights = None

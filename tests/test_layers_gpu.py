@@ -27,6 +27,7 @@ import torch
 
 from parity import relerr
 from flashslice_amd.layers import Physics_Attention_Irregular_Mesh, Transolver
+from flashslice_amd.layers.basic import PointLinear
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -75,6 +76,30 @@ def _compare(make, inputs, loss_fn, blocked=False):
     for n, f, e, t in zip(names, r_f, r_e, r_t):
         _gate(n, f, e, t, blocked)
     return r_f
+
+
+def test_point_linear_split_k():
+    """The per-point Linear's split-K weight gradient against nn.Linear's and
+    float64 (the same gate), on a row count that is no multiple of the chunk
+    count (the remainder path), and bitwise equal over two runs."""
+    torch.manual_seed(6)
+    M = 200_003
+    print("[point-linear] M=%d" % M, flush=True)
+    lin = PointLinear(256, 512).to(DEV)
+    ref = torch.nn.Linear(256, 512).to(DEV)
+    ref.load_state_dict(lin.state_dict())
+    truth = copy.deepcopy(ref).double()
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(1, M, 256, generator=g).to(DEV)
+    up = torch.randn(1, M, 512, generator=g).to(DEV)
+    loss = lambda out: (out * up.to(out.dtype)).sum()  # noqa: E731
+    r1 = _run(lin, [x], loss)
+    r2 = _run(lin, [x], loss)
+    assert all(torch.equal(a, b) for a, b in zip(r1, r2))
+    re_ = _run(ref, [x], loss)
+    rt = _run(truth, [x.double()], loss)
+    for n, a, b, t in zip(["out", "weight", "bias", "x"], r1, re_, rt):
+        _gate(n, a, b, t)
 
 
 def _mse(target):
