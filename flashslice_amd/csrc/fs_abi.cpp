@@ -7,6 +7,7 @@
 // on every run and every GPU), carves the caller's workspace, launches the
 // point-streaming kernels and then the fixed-order reduction of their
 // partials. Nothing here allocates, frees or synchronises.
+#include <initializer_list>
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -644,6 +645,55 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
   }
   rs.n = 4;
   return hip_check(fs::launch_reduce((int)p->B, (int)p->H, rs, st), who);
+}
+
+// ------------------------------------------------------------- LayerNorm
+// The layer's normalisation of (rows, cols) fp32 rows (fs_layernorm.hip).
+static int32_t ln_check(const char* who, int64_t rows, int32_t cols,
+                        std::initializer_list<const void*> ptrs) {
+  if (rows < 1) return fail(FS_ERR_INVALID, "%s: rows must be >= 1 (got %lld)", who, (long long)rows);
+  if (cols < 4 || cols > 2048 || cols % 4)
+    return fail(FS_ERR_INVALID, "%s: cols must be a multiple of 4 in [4, 2048] (got %d)", who,
+                (int)cols);
+  for (const void* q : ptrs) {
+    if (!q) return fail(FS_ERR_INVALID, "%s: a tensor pointer is NULL", who);
+    if (reinterpret_cast<uintptr_t>(q) % 16)
+      return fail(FS_ERR_INVALID, "%s: tensors must be 16-byte aligned", who);
+  }
+  return FS_OK;
+}
+
+size_t fs_layernorm_workspace_bytes(int64_t rows, int32_t cols) {
+  if (rows < 1 || cols < 4 || cols > 2048 || cols % 4) return 0;
+  return (size_t)fs::ln_blocks(rows) * 2 * (size_t)cols * sizeof(float);
+}
+
+int32_t fs_layernorm_fwd(const float* x, const float* gamma, const float* beta, float* y,
+                         float* mean, float* rstd, int64_t rows, int32_t cols, float eps,
+                         void* stream) {
+  const char* who = "fs_layernorm_fwd";
+  int32_t rc = ln_check(who, rows, cols, {x, gamma, beta, y});
+  if (rc) return rc;
+  if (!mean || !rstd) return fail(FS_ERR_INVALID, "%s: mean / rstd is NULL", who);
+  return hip_check(fs::ln_fwd_launch(x, gamma, beta, y, mean, rstd, rows, cols, eps,
+                                     (hipStream_t)stream), who);
+}
+
+int32_t fs_layernorm_bwd(const float* dy, const float* x, const float* gamma, const float* mean,
+                         const float* rstd, float* dx, float* dgamma, float* dbeta,
+                         void* workspace, size_t workspace_bytes, int64_t rows, int32_t cols,
+                         void* stream) {
+  const char* who = "fs_layernorm_bwd";
+  int32_t rc = ln_check(who, rows, cols, {dy, x, gamma, dx, workspace});
+  if (rc) return rc;
+  if (!mean || !rstd || !dgamma || !dbeta)
+    return fail(FS_ERR_INVALID, "%s: mean / rstd / dgamma / dbeta is NULL", who);
+  if (workspace_bytes < fs_layernorm_workspace_bytes(rows, cols))
+    return fail(FS_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed", who, workspace_bytes,
+                fs_layernorm_workspace_bytes(rows, cols));
+  return hip_check(fs::ln_bwd_launch(dy, x, gamma, mean, rstd, dx, dgamma, dbeta,
+                                     static_cast<float*>(workspace), rows, cols,
+                                     (hipStream_t)stream), who);
 }
 
 }  // extern "C"

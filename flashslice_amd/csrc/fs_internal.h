@@ -133,4 +133,13 @@ struct ReduceSegments {
 };
 hipError_t launch_reduce(int B, int H, const ReduceSegments& segs, hipStream_t st);
 
+// LayerNorm of (rows, C) fp32 rows (fs_layernorm.hip); C % 4 == 0, C <= 2048.
+int64_t ln_blocks(int64_t rows);
+hipError_t ln_fwd_launch(const float* x, const float* gamma, const float* beta, float* y,
+                         float* mean, float* rstd, int64_t rows, int C, float eps,
+                         hipStream_t st);
+hipError_t ln_bwd_launch(const float* dy, const float* x, const float* gamma, const float* mean,
+                         const float* rstd, float* dx, float* dgamma, float* dbeta, float* part,
+                         int64_t rows, int C, hipStream_t st);
+
 }  // namespace fs

@@ -22,7 +22,9 @@ _DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
 #: every entry point the header declares
 EXPORTS = ("fs_workspace_bytes", "fs_compute_stats", "fs_slice_fwd", "fs_deslice_fwd",
-           "fs_slice_bwd", "fs_deslice_bwd", "fs_family", "fs_last_error", "fs_version")
+           "fs_slice_bwd", "fs_deslice_bwd", "fs_family", "fs_last_error", "fs_version",
+           # the layer around the path (include/flashslice_layer.h)
+           "fs_layernorm_fwd", "fs_layernorm_bwd", "fs_layernorm_workspace_bytes")
 
 
 class FsPoints(ctypes.Structure):
@@ -70,6 +72,13 @@ def _declare(lib):
     lib.fs_last_error.restype = ctypes.c_char_p
     lib.fs_version.argtypes = []
     lib.fs_version.restype = ctypes.c_char_p
+    I64, F32 = ctypes.c_int64, ctypes.c_float
+    lib.fs_layernorm_fwd.argtypes = [V, V, V, V, V, V, I64, I32, F32, V]
+    lib.fs_layernorm_fwd.restype = I32
+    lib.fs_layernorm_workspace_bytes.argtypes = [I64, I32]
+    lib.fs_layernorm_workspace_bytes.restype = S
+    lib.fs_layernorm_bwd.argtypes = [V, V, V, V, V, V, V, V, V, S, I64, I32, V]
+    lib.fs_layernorm_bwd.restype = I32
 
 
 def lib():

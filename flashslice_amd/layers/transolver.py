@@ -22,6 +22,7 @@ import torch.nn as nn
 from torch.nn.init import trunc_normal_
 
 from .basic import MLP, PointLinear
+from .norm import PointLayerNorm
 from .physics_attention import TOKEN_EPS, Physics_Attention_Irregular_Mesh
 
 
@@ -35,7 +36,7 @@ class TransolverBlock(nn.Module):
                  slice_dim_head=None, use_fused_slice=False):
         super().__init__()
         self.last_layer, self.mlp_only = last_layer, mlp_only
-        self.ln_1 = nn.LayerNorm(hidden_dim)
+        self.ln_1 = PointLayerNorm(hidden_dim)
         if not mlp_only:
             self.Attn = Physics_Attention_Irregular_Mesh(
                 hidden_dim, heads=num_heads,
@@ -43,11 +44,11 @@ class TransolverBlock(nn.Module):
                 dropout=dropout, slice_num=slice_num, untied_deslice=untied_deslice,
                 no_token_attention=no_token_attention, slice_dim_head=slice_dim_head,
                 use_fused_slice=use_fused_slice)
-        self.ln_2 = nn.LayerNorm(hidden_dim)
+        self.ln_2 = PointLayerNorm(hidden_dim)
         self.mlp = MLP(hidden_dim, hidden_dim * mlp_ratio, hidden_dim, n_layers=0, res=False,
                        act=act)
         if last_layer:
-            self.ln_3 = nn.LayerNorm(hidden_dim)
+            self.ln_3 = PointLayerNorm(hidden_dim)
             self.mlp2 = PointLinear(hidden_dim, out_dim)
 
     def forward(self, fx, slice_weights_in=None):

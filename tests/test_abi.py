@@ -1,7 +1,7 @@
 """The C ABI library (CPU-only checks: no kernel is launched).
 
-* the in-tree library loads and exports every entry point that
-  ``include/flashslice_hip.h`` declares;
+* the in-tree library loads and exports every entry point that the headers
+  in ``include/`` declare;
 * argument validation happens before any launch and reports through
   ``fs_last_error`` (these calls never reach the GPU);
 * workspace sizing and family routing are pure functions of the shape.
@@ -17,11 +17,11 @@ import torch
 from flashslice_amd.kernels import _hip
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "flashslice_hip.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("flashslice_hip.h", "flashslice_layer.h")]
 
 
 def _declared():
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     return sorted(set(re.findall(r"\b(fs_[a-z_]+)\s*\(", text)))
 
 
@@ -129,3 +129,24 @@ def test_family_routing():
                             ((32, 32, 256), 2), ((32, 32, 1024), 2), ((256, 32, 32), 2)):
         p, keep = _params(D=D, DV=DV, G=G)
         assert lib.fs_family(ctypes.byref(p)) == fam, (D, DV, G)
+
+
+def test_layernorm_validation_before_launch():
+    """The layer's LayerNorm entry points (include/flashslice_layer.h):
+    workspace sizing is a function of the shape, and bad shapes or pointers
+    are refused before any launch."""
+    lib = _hip.lib()
+    assert lib.fs_layernorm_workspace_bytes(2_000_000, 256) > 0
+    assert lib.fs_layernorm_workspace_bytes(2_000_000, 258) == 0
+    assert lib.fs_layernorm_workspace_bytes(0, 256) == 0
+    assert lib.fs_layernorm_workspace_bytes(10, 4096) == 0
+    V = ctypes.c_void_p
+    p = V(4096)  # never dereferenced: validation fails first
+    rc = lib.fs_layernorm_fwd(p, p, p, p, p, p, 100, 6, 1e-5, None)
+    assert rc == _hip.FS_ERR_INVALID and b"multiple of 4" in lib.fs_last_error()
+    rc = lib.fs_layernorm_fwd(p, None, p, p, p, p, 100, 256, 1e-5, None)
+    assert rc == _hip.FS_ERR_INVALID and b"NULL" in lib.fs_last_error()
+    rc = lib.fs_layernorm_fwd(V(4100), p, p, p, p, p, 100, 256, 1e-5, None)
+    assert rc == _hip.FS_ERR_INVALID and b"aligned" in lib.fs_last_error()
+    rc = lib.fs_layernorm_bwd(p, p, p, p, p, p, p, p, p, 0, 100, 256, None)
+    assert rc == _hip.FS_ERR_WORKSPACE

@@ -28,6 +28,7 @@ import torch
 from parity import relerr
 from flashslice_amd.layers import Physics_Attention_Irregular_Mesh, Transolver
 from flashslice_amd.layers.basic import PointLinear
+from flashslice_amd.layers.norm import PointLayerNorm
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -95,6 +96,34 @@ def test_point_linear_split_k():
     loss = lambda out: (out * up.to(out.dtype)).sum()  # noqa: E731
     r1 = _run(lin, [x], loss)
     r2 = _run(lin, [x], loss)
+    assert all(torch.equal(a, b) for a, b in zip(r1, r2))
+    re_ = _run(ref, [x], loss)
+    rt = _run(truth, [x.double()], loss)
+    for n, a, b, t in zip(["out", "weight", "bias", "x"], r1, re_, rt):
+        _gate(n, a, b, t)
+
+
+@pytest.mark.parametrize("C", [256, 512])
+def test_point_layernorm(C):
+    """The HIP LayerNorm (include/flashslice_layer.h) against nn.LayerNorm and
+    float64 (the same gate) for output and every gradient, on an odd row
+    count, with a non-trivial affine; bitwise equal over two runs."""
+    torch.manual_seed(8)
+    M = 200_003
+    print("[layernorm] M=%d C=%d" % (M, C), flush=True)
+    ln = PointLayerNorm(C).to(DEV)
+    with torch.no_grad():
+        ln.weight.uniform_(0.5, 1.5)
+        ln.bias.uniform_(-0.2, 0.2)
+    ref = torch.nn.LayerNorm(C).to(DEV)
+    ref.load_state_dict(ln.state_dict())
+    truth = copy.deepcopy(ref).double()
+    g = torch.Generator().manual_seed(9)
+    x = (3.0 + 2.0 * torch.randn(M, C, generator=g)).to(DEV)
+    up = torch.randn(M, C, generator=g).to(DEV)
+    loss = lambda out: (out * up.to(out.dtype)).sum()  # noqa: E731
+    r1 = _run(ln, [x], loss)
+    r2 = _run(ln, [x], loss)
     assert all(torch.equal(a, b) for a, b in zip(r1, r2))
     re_ = _run(ref, [x], loss)
     rt = _run(truth, [x.double()], loss)
