@@ -21,6 +21,15 @@ from ..kernels import _hip
 
 MIN_ROWS = 65536
 
+# Custom operators (own namespace; the reference defines none for this), so
+# that torch.compile keeps them as single opaque nodes: the CUDA-key
+# implementations call the C entry points, the fakes give shapes and dtypes.
+_LIB = torch.library.Library("flashslice_layer", "DEF")
+_LIB.define("layer_norm(Tensor x, Tensor weight, Tensor bias, float eps) "
+            "-> (Tensor, Tensor, Tensor)")
+_LIB.define("layer_norm_bwd(Tensor dy, Tensor x, Tensor weight, Tensor mean, Tensor rstd) "
+            "-> (Tensor, Tensor, Tensor)")
+
 
 def _ptr(t):
     return ctypes.c_void_p(t.data_ptr())
@@ -30,35 +39,64 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-class _LayerNormFn(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, weight, bias, eps):
-        C = x.shape[-1]
-        rows = x.numel() // C
-        y = torch.empty_like(x)
-        mean = torch.empty(rows, device=x.device, dtype=torch.float32)
-        rstd = torch.empty_like(mean)
-        _hip.check(_hip.lib().fs_layernorm_fwd(
-            _ptr(x), _ptr(weight), _ptr(bias), _ptr(y), _ptr(mean), _ptr(rstd), rows, C,
-            float(eps), _stream()))
-        ctx.save_for_backward(x, weight, mean, rstd)
-        return y
+def _ln_impl(x, weight, bias, eps):
+    """x (..., C) contiguous fp32 -> y, mean (rows,), rstd (rows,)."""
+    C = x.shape[-1]
+    rows = x.numel() // C
+    y = torch.empty_like(x)
+    mean = torch.empty(rows, device=x.device, dtype=torch.float32)
+    rstd = torch.empty_like(mean)
+    _hip.check(_hip.lib().fs_layernorm_fwd(
+        _ptr(x), _ptr(weight), _ptr(bias), _ptr(y), _ptr(mean), _ptr(rstd), rows, C,
+        float(eps), _stream()))
+    return y, mean, rstd
 
-    @staticmethod
-    def backward(ctx, gy):
-        x, weight, mean, rstd = ctx.saved_tensors
-        gy = gy.contiguous()
-        C = x.shape[-1]
-        rows = x.numel() // C
-        dx = torch.empty_like(x)
-        dw = torch.empty_like(weight)
-        db = torch.empty_like(weight)
-        nws = _hip.lib().fs_layernorm_workspace_bytes(rows, C)
-        ws = torch.empty(nws, device=x.device, dtype=torch.uint8)
-        _hip.check(_hip.lib().fs_layernorm_bwd(
-            _ptr(gy), _ptr(x), _ptr(weight), _ptr(mean), _ptr(rstd), _ptr(dx), _ptr(dw),
-            _ptr(db), _ptr(ws), nws, rows, C, _stream()))
-        return dx, dw, db, None
+
+def _ln_bwd_impl(dy, x, weight, mean, rstd):
+    C = x.shape[-1]
+    rows = x.numel() // C
+    dx = torch.empty_like(x)
+    dw = torch.empty_like(weight)
+    db = torch.empty_like(weight)
+    nws = _hip.lib().fs_layernorm_workspace_bytes(rows, C)
+    ws = torch.empty(nws, device=x.device, dtype=torch.uint8)
+    _hip.check(_hip.lib().fs_layernorm_bwd(
+        _ptr(dy), _ptr(x), _ptr(weight), _ptr(mean), _ptr(rstd), _ptr(dx), _ptr(dw), _ptr(db),
+        _ptr(ws), nws, rows, C, _stream()))
+    return dx, dw, db
+
+
+_LIB.impl("layer_norm", _ln_impl, "CUDA")
+_LIB.impl("layer_norm_bwd", _ln_bwd_impl, "CUDA")
+
+
+@torch.library.register_fake("flashslice_layer::layer_norm")
+def _(x, weight, bias, eps):
+    rows = x.numel() // x.shape[-1]
+    return (torch.empty_like(x), x.new_empty(rows, dtype=torch.float32),
+            x.new_empty(rows, dtype=torch.float32))
+
+
+@torch.library.register_fake("flashslice_layer::layer_norm_bwd")
+def _(dy, x, weight, mean, rstd):
+    return torch.empty_like(x), torch.empty_like(weight), torch.empty_like(weight)
+
+
+def _ln_setup(ctx, inputs, output):
+    x, weight, _, _ = inputs
+    _, mean, rstd = output
+    ctx.save_for_backward(x, weight, mean, rstd)
+
+
+def _ln_grad(ctx, gy, gmean, grstd):
+    x, weight, mean, rstd = ctx.saved_tensors
+    dx, dw, db = torch.ops.flashslice_layer.layer_norm_bwd(gy.contiguous(), x, weight, mean,
+                                                           rstd)
+    return dx, dw, db, None
+
+
+torch.library.register_autograd("flashslice_layer::layer_norm", _ln_grad,
+                                setup_context=_ln_setup)
 
 
 class PointLayerNorm(nn.LayerNorm):
@@ -74,6 +112,7 @@ class PointLayerNorm(nn.LayerNorm):
 
     def forward(self, x):
         if self._hip_ok(x):
-            return _LayerNormFn.apply(x.contiguous(), self.weight.contiguous(),
-                                      self.bias.contiguous(), self.eps)
+            y, _, _ = torch.ops.flashslice_layer.layer_norm(
+                x.contiguous(), self.weight.contiguous(), self.bias.contiguous(), self.eps)
+            return y
         return super().forward(x)

@@ -147,3 +147,23 @@ def test_ablations_run_eager(flag):
     y = m(torch.rand(2, 9, 3), torch.randn(2, 9, 2))
     assert y.shape == (2, 9, 2) and torch.isfinite(y).all()
     y.square().mean().backward()
+
+
+def test_layernorm_op_compiles_to_one_graph():
+    """The HIP LayerNorm is a custom operator with a fake: torch.compile traces
+    it (forward and the registered backward's shapes) without graph breaks,
+    on meta tensors so that no kernel runs."""
+    import torch._dynamo
+    import flashslice_amd.layers.norm  # noqa: F401 -- registers the operators
+
+    def f(x, w, b):
+        y, _, _ = torch.ops.flashslice_layer.layer_norm(x, w, b, 1e-5)
+        return y * 2.0
+
+    torch._dynamo.reset()
+    x = torch.empty(70000, 256, device="meta")
+    w = torch.empty(256, device="meta")
+    explain = torch._dynamo.explain(f)(x, w, w)
+    assert explain.graph_break_count == 0, explain.break_reasons
+    y, mean, rstd = torch.ops.flashslice_layer.layer_norm(x, w, w, 1e-5)
+    assert y.shape == x.shape and mean.shape == (70000,) and rstd.dtype == torch.float32
