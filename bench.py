@@ -96,7 +96,9 @@ def alg_bytes(B, N, H, D, DV, e=4):
     writes dx, dfx."""
     pts = B * N * H
     return {"slice_fwd": pts * (D + DV) * e, "deslice_fwd": pts * (D + DV) * e,
-            "deslice_bwd": pts * (2 * D + DV) * e, "slice_bwd": pts * (2 * D + 2 * DV) * e}
+            "deslice_bwd": pts * (2 * D + DV) * e, "slice_bwd": pts * (2 * D + 2 * DV) * e,
+            # the tied backward (--tied): reads x, fx, d_out, writes dx, dfx
+            "tied_bwd": pts * (2 * D + 3 * DV) * e}
 
 
 def alg_flops(B, N, H, D, DV, G):
@@ -105,7 +107,9 @@ def alg_flops(B, N, H, D, DV, G):
     u = 2 * B * N * H * G
     return {"slice_fwd": u * (D + DV), "deslice_fwd": u * (D + DV),
             "deslice_bwd": u * (3 * D + 2 * DV),  # logits, dtokens, omega, dx, dW
-            "slice_bwd": u * (3 * D + 2 * DV)}
+            "slice_bwd": u * (3 * D + 2 * DV),
+            # logits, omega (two value dots), dfx, dtokens, dx, dW
+            "tied_bwd": u * (3 * D + 4 * DV)}
 
 
 def measured_traffic(workload):
@@ -136,7 +140,7 @@ OPS = ("slice_fwd", "deslice_fwd", "deslice_bwd", "slice_bwd")
 
 
 def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", dot=0,
-             blocked=False, ev=None):
+             blocked=False, ev=None, tied=False):
     """One coupling step, forward and backward, through the operators the
     public API routes the shape to (reference slice_ops.py:961-1022): the
     single-tile ops, or (``blocked``) the blocked ops, which carry the
@@ -146,7 +150,10 @@ def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", dot=0
     given tokens are deslided, then the points are slided again (config 4's
     persistent point stream), and the backward runs in autograd's order
     (slice, then deslice). ``ev``: a (start, end) event pair per op name,
-    recorded around exactly that op."""
+    recorded around exactly that op. ``tied`` (deslice-first only): the
+    backward is the one tied operator (flashslice::deslice_slice_bwd, one
+    pass for both ops' gradients and a single dx) instead of the two
+    backward ops, whose two dx autograd would still have to add."""
     ops = torch.ops.flashslice
 
     def timed(name, fn, *args):
@@ -171,6 +178,10 @@ def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", dot=0
     if order == "deslice-first":
         out, st = timed("deslice_fwd", deslice_f, tok0, None)
         z, s, _ = timed("slice_fwd", slice_f, st)
+        if tied:
+            dx, dfx, dW, db, dt, dtok = timed("tied_bwd", ops.deslice_slice_bwd, x, fx, W, b,
+                                              tau, tok0, d_out, dzb, dsb, dot)
+            return z, s, out, dx, dtok, dW, db, dt, dfx
         dx2, dfx, dW2, db2, dt2 = timed("slice_bwd", slice_b, st, dzb, dsb)
         dx1, dtok, dW1, db1, dt1 = timed("deslice_bwd", deslice_b, tok0, st)
         return z, s, out, dx1, dtok, dW1, db1, dt1, dx2, dfx, dW2, db2, dt2
@@ -349,6 +360,9 @@ def main():
     ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS) + sorted(MODEL_WORKLOADS))
     ap.add_argument("--dot", default="ieee", choices=sorted(DOTS),
                     help="dot level: ieee (fp32 inputs) or bf16 (x_mid, fx_mid, W in bf16)")
+    ap.add_argument("--tied", action="store_true",
+                    help="deslice-first workloads: the backward as the tied operator "
+                         "(fused_deslice_slice's single pass) instead of the two backward ops")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="before the warmup, copy x once (B*N*H*D*4 bytes read and written): "
@@ -380,7 +394,12 @@ def main():
             inputs[i] = inputs[i].bfloat16()
     from flashslice_amd.kernels.slice_ops import _use_blocked
     blocked = _use_blocked(D, G, DV, dot)
-    run_step = functools.partial(step_ops, *inputs, order=order, dot=dot, blocked=blocked)
+    if a.tied and order != "deslice-first":
+        print("--tied applies to the deslice-first workloads (c4)", file=sys.stderr)
+        sys.exit(2)
+    ops_timed = (("deslice_fwd", "slice_fwd", "tied_bwd") if a.tied else OPS)
+    run_step = functools.partial(step_ops, *inputs, order=order, dot=dot, blocked=blocked,
+                                 tied=a.tied)
     torch.cuda.synchronize()
     print("[bench] %s; library %s" % (desc, _hip.lib().fs_version().decode()),
           file=sys.stderr, flush=True)
@@ -415,7 +434,7 @@ def main():
 
     # timed region: K steps, per-op HIP events on the launch stream
     evs = [{n: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for n in OPS} for _ in range(a.steps)]
+            for n in ops_timed} for _ in range(a.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(a.steps):
@@ -423,14 +442,16 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = 1e3 * wall / a.steps
-    per_op = {n: sum(e[n][0].elapsed_time(e[n][1]) for e in evs) / a.steps for n in OPS}
+    per_op = {n: sum(e[n][0].elapsed_time(e[n][1]) for e in evs) / a.steps for n in ops_timed}
     bytes_ = alg_bytes(B, N, H, D, DV, 2 if a.dot == "bf16" else 4)
     flops = alg_flops(B, N, H, D, DV, G)
     dom = max(per_op, key=per_op.get)
     ach = bytes_[dom] / (per_op[dom] * 1e-3) / 1e9
     ach_tf = flops[dom] / (per_op[dom] * 1e-3) / 1e12
-    total_bytes = sum(bytes_.values())
-    total_flops = sum(flops.values())
+    # the step's algorithmic units are the four ops' (the metric's unit),
+    # whichever form the backward takes
+    total_bytes = sum(bytes_[n] for n in OPS)
+    total_flops = sum(flops[n] for n in OPS)
     step_ach = total_bytes / (ms_step * 1e-3) / 1e9
     traffic = measured_traffic(a.workload)
 
@@ -453,7 +474,8 @@ def main():
         "dtype": "f32" if a.dot == "ieee" else "bf16", "data": "synthetic",
         "config": {"workload": desc, "B": B, "N": N, "H": H, "D": D, "DV": DV, "G": G,
                    "weight": layout, "order": order, "dot": a.dot,
-                   "ops": "blocked" if blocked else "single-tile"},
+                   "ops": "blocked" if blocked else "single-tile",
+                   "backward": "tied" if a.tied else "two ops"},
         "roofline": ({"bound": "hbm", "kernel": dom, "achieved": round(ach, 1),
                       "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4)}
                      if a.workload == "c2" else
@@ -472,7 +494,7 @@ def main():
         "cpu_baseline": cpu,
     }
     line["roofline"].update({
-        "traffic": traffic.get(dom) if traffic else None,
+        "traffic": traffic.get(dom) if traffic and not a.tied else None,
         "alg_bytes_per_launch": bytes_[dom], "alg_flops_per_launch": flops[dom],
         "ms_per_launch": round(per_op[dom], 4)})
     print(json.dumps(line), flush=True)

@@ -29,7 +29,7 @@ SOURCES = ("fs_fused.hip", "fs_blocked.hip", "fs_reduce.hip", "fs_layernorm.hip"
 # explicit instances of fused_launch<K, T, DK> (fs_fused_kernels.h), one
 # generated translation unit each so that they compile in parallel
 _FUSED_TYPES = (("float", (0,)), ("__bf16", (0, 1, 2)), ("_Float16", (0, 1, 2)))
-FUSED_INSTANCES = tuple((k, t, dk) for k in range(4) for t, dks in _FUSED_TYPES for dk in dks)
+FUSED_INSTANCES = tuple((k, t, dk) for k in range(5) for t, dks in _FUSED_TYPES for dk in dks)
 # and of blocked_launch<K, T, DK> (fs_blocked_kernels.h)
 BLOCKED_INSTANCES = tuple((k, t, dk) for k in range(8) for t, dks in _FUSED_TYPES for dk in dks)
 FLAGS = [

@@ -100,6 +100,7 @@ int64_t fused_target(int32_t op, const fs_slice_params* p) {
   const bool one = p->G <= 32 && p->D <= 32 && p->DV <= 32;
   switch (op) {
     case FS_OP_DESLICE_BWD: return 512;
+    case FS_OP_TIED_BWD: return 512;
     case FS_OP_SLICE_FWD: return one ? 1536 : 512;
     case FS_OP_DESLICE_FWD: return one ? 2048 : 1536;
     default: return 1536;
@@ -227,6 +228,7 @@ int64_t wave_floats(int32_t op, const fs_slice_params* p) {
     case FS_OP_SLICE_FWD: return fs::part_floats_slice_fwd(G, DV);
     case FS_OP_SLICE_BWD: return fs::part_floats_slice_bwd(G, D);
     case FS_OP_DESLICE_BWD: return fs::part_floats_deslice_bwd(G, D, DV);
+    case FS_OP_TIED_BWD: return fs::part_floats_deslice_bwd(G, D, DV);
     default: return 0;
   }
 }
@@ -263,7 +265,9 @@ Workspace plan_ws(int32_t op, const fs_slice_params* p, char* base) {
   if (blocked && gp_on(p))
     w.frags = take((size_t)fs::gp_layout((int)p->B, (int)p->H, (int)p->G, (int)p->D, (int)p->DV,
                                          0).total_u32x4 * 4);
-  if (op == FS_OP_DESLICE_FWD || op == FS_OP_STATS) {
+  // the tied backward runs on the whole-G family only (else unsupported)
+  if (op == FS_OP_DESLICE_FWD || op == FS_OP_STATS ||
+      (op == FS_OP_TIED_BWD && family_of(p) != 1)) {
     w.bytes = off;
     return w;
   }
@@ -643,6 +647,66 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
     rs.seg[2] = seg(ws.part, wf, offB, gg.P, G, Bb, Hb, dbias);
     rs.seg[3] = seg(ws.part2, 1, 0, gn.P, 1, 1, (int)p->H, dtau);
   }
+  rs.n = 4;
+  return hip_check(fs::launch_reduce((int)p->B, (int)p->H, rs, st), who);
+}
+
+int32_t fs_tied_bwd(const fs_points* x, const fs_points* fx, const fs_points* d_out,
+                    const fs_slice_params* p, const float* tokens, const float* dz_num,
+                    const float* ds, const fs_points* dx, const fs_points* dfx,
+                    float* dtokens, float* dweight, float* dbias, float* dtau,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  const char* who = "fs_tied_bwd";
+  int32_t rc = check_params(p, who);
+  if (!rc) rc = check_points(x, "x_mid", p->D, who);
+  if (!rc) rc = check_points(fx, "fx_mid", p->DV, who);
+  if (!rc) rc = check_points(d_out, "d_out", p->DV, who);
+  if (!rc) rc = check_out_points(dx, "dx", p->D, who);
+  if (!rc) rc = check_out_points(dfx, "dfx", p->DV, who);
+  if (rc) return rc;
+  if (fx->dtype != x->dtype || d_out->dtype != x->dtype || dx->dtype != x->dtype ||
+      dfx->dtype != x->dtype)
+    return fail(FS_ERR_INVALID, "%s: point tensors must share one dtype", who);
+  if (!tokens || !dz_num || !ds || !dtokens || !dweight || !dbias || !dtau)
+    return fail(FS_ERR_INVALID,
+                "%s: tokens, dz_num, ds, dtokens, dweight, dbias, dtau must be non-NULL", who);
+  if (family_of(p) != 1)
+    return fail(FS_ERR_UNSUPPORTED,
+                "%s: served by the whole-G kernels only (G <= 128 and D, DV small enough); "
+                "run fs_deslice_bwd and fs_slice_bwd", who);
+  const Workspace ws = plan_ws(FS_OP_TIED_BWD, p, (char*)workspace);
+  rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  const int mode = mode_of(p->dot, x->dtype);
+  const int64_t wf = wave_floats(FS_OP_TIED_BWD, p);
+  const int G = (int)p->G, D = (int)p->D, DV = (int)p->DV;
+  const int64_t offW = (int64_t)G * DV, offB = offW + (int64_t)G * D;
+  const int Bw = Bo_of(p->w_stride_b, p->B), Hw = Ho_of(p->w_stride_h, p->H);
+  const int Bb = Bo_of(p->b_stride_b, p->B), Hb = Ho_of(p->b_stride_h, p->H);
+  const Geo g = geo_n(p, fused_target(FS_OP_TIED_BWD, p));
+  fs::Args a = base_args(p, g);
+  set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+  set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
+  set_in(d_out, &a.g, &a.sgb, &a.sgn, &a.sgh);
+  set_out(dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
+  set_out(dfx, &a.o2, &a.s2b, &a.s2n, &a.s2h);
+  a.vec_x = vec_ok(x);
+  a.vec_f = vec_ok(fx) && vec_ok(d_out);
+  a.vec_1 = vec_ok(dx);
+  a.vec_2 = vec_ok(dfx);
+  a.fast = a.vec_x && a.vec_f && a.vec_1 && a.vec_2 && full_widths(p);
+  a.tok = dz_num;
+  a.tok2 = tokens;
+  a.ds = ds;
+  a.part = ws.part;
+  rc = hip_check(fs::launch_fused_tied_bwd(a, x->dtype, mode, st), who);
+  if (rc) return rc;
+  fs::ReduceSegments rs{};
+  rs.seg[0] = seg(ws.part, wf, 0, pb(g), G * DV, (int)p->B, (int)p->H, dtokens);
+  rs.seg[1] = seg(ws.part, wf, offW, pb(g), G * D, Bw, Hw, dweight);
+  rs.seg[2] = seg(ws.part, wf, offB, pb(g), G, Bb, Hb, dbias);
+  rs.seg[3] = seg(ws.part, wf, offB + G, pb(g), 1, 1, (int)p->H, dtau);
   rs.n = 4;
   return hip_check(fs::launch_reduce((int)p->B, (int)p->H, rs, st), who);
 }

@@ -38,5 +38,8 @@ hipError_t launch_fused_slice_bwd(const Args& a, int dtype, int mode, hipStream_
 hipError_t launch_fused_deslice_bwd(const Args& a, int dtype, int mode, hipStream_t st) {
   return fused_dispatch<FK_DESLICE_BWD>(a, dtype, mode, st);
 }
+hipError_t launch_fused_tied_bwd(const Args& a, int dtype, int mode, hipStream_t st) {
+  return fused_dispatch<FK_TIED_BWD>(a, dtype, mode, st);
+}
 
 }  // namespace fs

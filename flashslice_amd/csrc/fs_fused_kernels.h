@@ -803,6 +803,243 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
   });
 }
 
+// ------------------------------------------------------------------- tied bwd
+// Backward of a deslice -> slice coupling on one x_mid, W, b, tau (out =
+// deslice(tokens), (z_num, s) = slice(fx); fx not computed from out), both
+// ops' gradients from one recompute of w per tile:
+//   dfx = w dz_num,  dtokens += w^T d_out,
+//   omega = fx . dz_num + ds + d_out . tokens  (the two Jacobian inputs:
+//   Lb = w (omega - sum_g w omega) is linear in omega, so one Jacobian, one
+//   dx = Lb W / tau, one dW += Lb^T x, db, dtau serve both ops).
+// Point traffic: reads x, fx, d_out, writes dx, dfx (5 passes) against the
+// two backward kernels' 4 + 3 and autograd's sum of their two dx (3 more).
+// Value fragments in LDS: dz_num [g, v] (omega) and [v, g] (dfx), tokens
+// [g, v] (omega), W / tau [d, g] (dx). Partials in the deslice-bwd layout.
+// One wave per SIMD for every shape (the slot accumulators of both ops).
+template <typename T, int DK, int NGB, int NDB, int NVB>
+__global__ __launch_bounds__(256, 1) void k_fused_tied_bwd(Args a) {
+  FS_PROLOGUE(NGB, NDB, NVB, 3 * NGB * NVB + NDB * NGB, kLdsTile)
+  static_assert(SM::TOTAL * 4 <= 160 * 1024, "tied backward LDS exceeds 160 KB");
+  u32x4* qZr = qV;
+  u32x4* qZc = qV + NGB * NVB * FWV;
+  u32x4* qTr = qV + 2 * NGB * NVB * FWV;
+  u32x4* qWc = qV + 3 * NGB * NVB * FWV;
+  build_frags<MV>(qZr, NGB * NVB, wid, lane, [&](int i, float(&f)[16]) {
+    lds_frag_rowouter(f, sV, SM::SV, 32 * (i / NVB), 32 * (i % NVB), c, h);
+  });
+  build_frags<MV>(qZc, NVB * NGB, wid, lane, [&](int i, float(&f)[16]) {
+    lds_frag_colouter(f, sV, SM::SV, 32 * (i % NGB), 32 * (i / NGB), c, h);
+  });
+  build_frags<MV>(qWc, NDB * NGB, wid, lane, [&](int i, float(&f)[16]) {
+    lds_frag_colouter(f, sW, SM::SW, 32 * (i % NGB), 32 * (i / NGB), c, h);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) f[j] *= inv_tau;
+  });
+  for (int i = threadIdx.x; i < SM::GP; i += 256) sDS[i] = i < G ? a.ds[(int64_t)bh * G + i] : 0.f;
+  // the staging area now takes the tokens (dz_num's fragments are built)
+  __syncthreads();
+  stage_matrix(sV, SM::SV, a.tok2 + (int64_t)bh * G * DV, G, DV, SM::GP, 32 * NVB);
+  __syncthreads();
+  build_frags<MV>(qTr, NGB * NVB, wid, lane, [&](int i, float(&f)[16]) {
+    lds_frag_rowouter(f, sV, SM::SV, 32 * (i / NVB), 32 * (i % NVB), c, h);
+  });
+  FS_PROLOGUE_END
+  f32x16 dT[NGB][NVB], dW[NGB][NDB];
+  float dbacc[NGB], dtacc = 0.f;
+#pragma unroll
+  for (int gb = 0; gb < NGB; ++gb) {
+    dbacc[gb] = 0.f;
+#pragma unroll
+    for (int vb = 0; vb < NVB; ++vb) dT[gb][vb] = zero16();
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) dW[gb][db] = zero16();
+  }
+  FS_SLICE(x, a.x, a.sxb, a.sxn, a.sxh, D)
+  FS_SLICE(f, a.f, a.sfb, a.sfn, a.sfh, DV)
+  FS_SLICE(g, a.g, a.sgb, a.sgn, a.sgh, DV)
+  FS_SLICE(dx, a.o1, a.s1b, a.s1n, a.s1h, D)
+  FS_SLICE(df, a.o2, a.s2b, a.s2n, a.s2h, DV)
+  (void)dx_row; (void)df_row;
+  uint32_t vcx[NDB], vcf[NVB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) vcx[db] = col_off<T>(db, D, dx_sn, c, h);
+#pragma unroll
+  for (int vb = 0; vb < NVB; ++vb) vcf[vb] = col_off<T>(vb, DV, df_sn, c, h);
+  auto run = [&](auto fast_c) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
+    const uint32_t vrf = FAST ? f_row + 4 * h * (uint32_t)sizeof(T) : f_row;
+    const uint32_t vrg = FAST ? g_row + 4 * h * (uint32_t)sizeof(T) : g_row;
+    // x is double-buffered; fx and d_out have one buffer each, reloaded
+    // once omega and d_out's transpose have consumed them
+    float xA[NDB][16], xB[NDB][16], ff[NVB][16], of[NVB][16];
+    auto load = [&](float (&xn)[NDB][16], int t) {
+      ld_rows<T, NDB, FAST>(xn, rows_rsrc_sel(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
+    };
+    auto load_f = [&](int t) {
+      ld_rows<T, NVB, FAST>(ff, rows_rsrc_sel(f_b, f_sn, f_w, (int64_t)t * kTile, N), vrf, DV, h);
+    };
+    auto load_g = [&](int t) {
+      ld_rows<T, NVB, FAST>(of, rows_rsrc_sel(g_b, g_sn, g_w, (int64_t)t * kTile, N), vrg, DV, h);
+    };
+    auto body = [&](const float (&xf)[NDB][16], int t, auto par) {
+      const int64_t p0 = (int64_t)t * kTile;
+      const bool pv = p0 + c < N;
+      constexpr float sg = decltype(par)::sign;
+      float t2[NGB][16], w[NGB][16], m2, lsum;
+      float om[NGB][16];
+      {
+        Frag<ML> xq[NDB];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xf[db]);
+        FS_LOGITS(t2, xq)
+      }
+      // each stage below is its own scheduling region: operand fragments are
+      // read from LDS next to their use rather than hoisted across stages
+      // (which runs the wider shapes out of registers)
+      sched_fence();
+      // omega = fx . dz_num + d_out . tokens + ds, one accumulator per slot
+      // block; one value block's split pieces live at a time
+      {
+        f32x16 o[NGB];
+#pragma unroll
+        for (int gb = 0; gb < NGB; ++gb) o[gb] = zero16();
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) {
+          Frag<MV> fq;
+          prep<MV>(fq, ff[vb]);
+#pragma unroll
+          for (int gb = 0; gb < NGB; ++gb) {
+            Frag<MV> zq;
+            lds_get<MV>(zq, qZr + (gb * NVB + vb) * FWV, lane);
+            o[gb] = mma<MV>(zq, fq, o[gb]);
+          }
+        }
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) {
+          Frag<MV> oq;
+          prep<MV>(oq, of[vb]);
+#pragma unroll
+          for (int gb = 0; gb < NGB; ++gb) {
+            Frag<MV> tq;
+            lds_get<MV>(tq, qTr + (gb * NVB + vb) * FWV, lane);
+            o[gb] = mma<MV>(tq, oq, o[gb]);
+          }
+        }
+#pragma unroll
+        for (int gb = 0; gb < NGB; ++gb) {
+          float dsv[16];  // d s per output slot
+          lds_frag_vec(dsv, sDS + 32 * gb, h);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) om[gb][r] = o[gb][r] + dsv[r];
+        }
+      }
+      sched_fence();
+      {
+        // d_out^T carrying the tile's sign (acc_add), split here when several
+        // slot blocks share it, else next to its one use
+        float oT[NVB][16];
+        Frag<MV> oTq[NVB];
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) {
+          transpose32(oT[vb], of[vb], lds, c, h);
+#pragma unroll
+          for (int j = 0; j < 16; ++j) oT[vb][j] *= sg;
+          if constexpr (NGB > 1) prep<MV>(oTq[vb], oT[vb]);
+        }
+        softmax_tile<NGB>(w, m2, lsum, t2, pv);
+        sched_fence();
+        // dtokens += w^T d_out (rows of d_out beyond N read as zero), first:
+        // d_out's transposed pieces die before dfx's accumulators are live
+#pragma unroll
+        for (int gb = 0; gb < NGB; ++gb) {
+          float wT[16];
+          transpose32(wT, w[gb], lds, c, h);
+          Frag<MV> wTq;
+          prep<MV>(wTq, wT);
+#pragma unroll
+          for (int vb = 0; vb < NVB; ++vb) {
+            if constexpr (NGB == 1) prep<MV>(oTq[vb], oT[vb]);
+            mma_acc<MV>(dT[gb][vb], oTq[vb], wTq, sg);
+          }
+        }
+        sched_fence();
+        // dfx = w dz_num (rows beyond N are not stored)
+        {
+          f32x16 o[NVB];
+#pragma unroll
+          for (int vb = 0; vb < NVB; ++vb) o[vb] = zero16();
+#pragma unroll
+          for (int gb = 0; gb < NGB; ++gb) {
+            Frag<MV> wq;
+            prep<MV>(wq, w[gb]);
+#pragma unroll
+            for (int vb = 0; vb < NVB; ++vb) {
+              Frag<MV> zq;
+              lds_get<MV>(zq, qZc + (vb * NGB + gb) * FWV, lane);
+              o[vb] = mma<MV>(wq, zq, o[vb]);
+            }
+          }
+          const Rsrc rdf = rows_rsrc_sel(df_b, df_sn, df_w, p0, N);
+#pragma unroll
+          for (int vb = 0; vb < NVB; ++vb) st_cols<T>(rdf, vcf[vb], (uint32_t)df_sn, o[vb]);
+        }
+        sched_fence();
+        dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
+        // fx and d_out are reloaded for the wave's next tile only now: from
+        // omega to here (the register peak) their buffers are dead, and dx,
+        // dW and the next tile's logits still cover the loads' latency
+        load_f(t + a.P);
+        load_g(t + a.P);
+        sched_fence();
+        FS_DX_DW(om, qWc, sg)
+      }
+    };
+    load_f(pid);
+    load_g(pid);
+    FS_TILE_LOOP(load, body, true, xA, xB)
+  };
+  if (fast) run(std::true_type()); else run(std::false_type());
+  float dbs[NGB];
+#pragma unroll
+  for (int gb = 0; gb < NGB; ++gb) dbs[gb] = pair_sum(dbacc[gb]) * inv_tau;
+  const float dt = -kLn2 * inv_tau * half_wave_sum(dtacc);
+  const int64_t offW = (int64_t)G * DV, E = part_floats_deslice_bwd(G, D, DV);
+  float* pw = a.part + ((int64_t)bh * gridDim.x + blockIdx.x) * E;
+  block_partial(smem, (int)offW, wid, pw, [&](float* buf, bool first) {
+#pragma unroll
+    for (int gb = 0; gb < NGB; ++gb) {
+      const int g = 32 * gb + c;
+      if (g < G) {
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int v = 32 * vb + kmap(r, h);
+            if (v < DV) acc_put(buf[g * DV + v], dT[gb][vb][r], first);
+          }
+      }
+    }
+  });
+  block_partial(smem, (int)(E - offW), wid, pw + offW, [&](float* buf, bool first) {
+#pragma unroll
+    for (int gb = 0; gb < NGB; ++gb) {
+      const int g = 32 * gb + c;
+      if (g < G) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int d = 32 * db + kmap(r, h);
+            if (d < D) acc_put(buf[g * D + d], dW[gb][db][r] * inv_tau, first);
+          }
+        if (h == 0) acc_put(buf[G * D + g], dbs[gb], first);
+      }
+    }
+    if (lane == 0) acc_put(buf[G * D + G], dt, first);
+  });
+}
+
 // ------------------------------------------------------------ launch templates
 // (NGB, NDB, NVB): slot, logits-width and value-width blocks of 32 held in
 // registers; the fused family serves shapes whose slot-indexed accumulators
@@ -811,7 +1048,13 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
   X(1, 1, 1) X(1, 1, 2) X(1, 1, 4) X(1, 2, 1) X(1, 2, 2) X(1, 2, 4) X(1, 4, 1) X(1, 4, 2) \
   X(1, 4, 4) X(2, 1, 1) X(2, 1, 2) X(2, 2, 1) X(2, 2, 2) X(4, 1, 1)
 
-enum FusedKind { FK_SLICE_FWD = 0, FK_DESLICE_FWD = 1, FK_SLICE_BWD = 2, FK_DESLICE_BWD = 3 };
+enum FusedKind {
+  FK_SLICE_FWD = 0,
+  FK_DESLICE_FWD = 1,
+  FK_SLICE_BWD = 2,
+  FK_DESLICE_BWD = 3,
+  FK_TIED_BWD = 4
+};
 
 __host__ inline int blocks_of(int n) {
   const int k = (n + 31) / 32;
@@ -833,6 +1076,8 @@ hipError_t fused_launch(const Args& a, hipStream_t st) {
       hipLaunchKernelGGL((k_fused_deslice_fwd<T, DK, G_, D_, V_>), grid, block, 0, st, a);    \
     else if constexpr (K == FK_SLICE_BWD)                                                     \
       hipLaunchKernelGGL((k_fused_slice_bwd<T, DK, G_, D_, V_>), grid, block, 0, st, a);      \
+    else if constexpr (K == FK_TIED_BWD)                                                      \
+      hipLaunchKernelGGL((k_fused_tied_bwd<T, DK, G_, D_, V_>), grid, block, 0, st, a);       \
     else                                                                                      \
       hipLaunchKernelGGL((k_fused_deslice_bwd<T, DK, G_, D_, V_>), grid, block, 0, st, a);    \
     return hipGetLastError();                                                                 \
@@ -850,7 +1095,9 @@ hipError_t fused_launch(const Args& a, hipStream_t st) {
   X(2, float, 0) X(2, __bf16, 0) X(2, __bf16, 1) X(2, __bf16, 2) X(2, _Float16, 0)   \
   X(2, _Float16, 1) X(2, _Float16, 2)                                                \
   X(3, float, 0) X(3, __bf16, 0) X(3, __bf16, 1) X(3, __bf16, 2) X(3, _Float16, 0)   \
-  X(3, _Float16, 1) X(3, _Float16, 2)
+  X(3, _Float16, 1) X(3, _Float16, 2)                                                \
+  X(4, float, 0) X(4, __bf16, 0) X(4, __bf16, 1) X(4, __bf16, 2) X(4, _Float16, 0)   \
+  X(4, _Float16, 1) X(4, _Float16, 2)
 
 #define FS_DECLARE_EXTERN(K_, T_, DK_) \
   extern template hipError_t fused_launch<K_, T_, DK_>(const Args&, hipStream_t);

@@ -18,10 +18,12 @@ struct Args {
   const void* f;  int64_t sfb, sfn, sfh;   // fx_mid or d_out (B, N, H, DV)
   void* o1;       int64_t s1b, s1n, s1h;   // out (deslice fwd) or dx (bwd)
   void* o2;       int64_t s2b, s2n, s2h;   // dfx (slice bwd)
+  const void* g;  int64_t sgb, sgn, sgh;   // d_out of the tied backward (B, N, H, DV)
   const float* W;    int64_t swb, swh;     // (.., G, D)
   const float* bias; int64_t sbb, sbh;     // (.., G)
   const float* tau;                        // (H,)
   const float* tok;                        // (B, H, G, DV): tokens or dz_num
+  const float* tok2;                       // (B, H, G, DV): tokens of the tied backward
   const float* ds;                         // (B, H, G): d s (slice bwd)
   const float* stats_in;                   // (B, H, 2, N) or null
   float* stats_out;                        // (B, H, 2, N) or null
@@ -96,6 +98,9 @@ hipError_t launch_fused_slice_fwd(const Args& a, int dtype, int mode, hipStream_
 hipError_t launch_fused_deslice_fwd(const Args& a, int dtype, int mode, hipStream_t st);
 hipError_t launch_fused_slice_bwd(const Args& a, int dtype, int mode, hipStream_t st);
 hipError_t launch_fused_deslice_bwd(const Args& a, int dtype, int mode, hipStream_t st);
+// backward of a deslice -> slice coupling in one pass; partials in the
+// deslice-bwd layout (dtokens, dW, db, dtau)
+hipError_t launch_fused_tied_bwd(const Args& a, int dtype, int mode, hipStream_t st);
 bool fused_fits(int D, int DV, int G);
 
 // G-blocked family (any G; fs_blocked.hip). Point-owned kernels ("_n") run

@@ -9,7 +9,9 @@ implementations call hand-written HIP kernels through the C ABI of
 implementation.
 
 The eleven public names are those of the reference package
-(``flashslice/kernels/__init__.py:44-59``).
+(``flashslice/kernels/__init__.py:44-59``); ``fused_deslice_slice`` (a
+deslice -> slice coupling with one fused backward pass, ``tied.py``) is an
+addition.
 """
 
 from .slice_ops import (
@@ -24,7 +26,8 @@ from .slice_ops import (
 )
 from . import blocked  # noqa: F401  -- registers the flashslice::*_blk ops
 from .blocked import set_block_g, set_stats_mode, stats_mode
+from .tied import fused_deslice_slice
 
 __all__ = ["fused_slice", "fused_deslice", "unsupported_dims", "single_tile_dims",
            "set_dot_mode", "set_kernel_mode", "set_block_g", "set_stats_mode",
-           "stats_mode", "set_tile_table", "tile_table"]
+           "stats_mode", "set_tile_table", "tile_table", "fused_deslice_slice"]

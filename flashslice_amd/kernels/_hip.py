@@ -16,13 +16,14 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__
                         "_lib", "libflashslice_hip.so")
 
 FS_OK, FS_ERR_INVALID, FS_ERR_UNSUPPORTED, FS_ERR_WORKSPACE, FS_ERR_HIP = range(5)
-OP_SLICE_FWD, OP_DESLICE_FWD, OP_SLICE_BWD, OP_DESLICE_BWD, OP_STATS = range(5)
+OP_SLICE_FWD, OP_DESLICE_FWD, OP_SLICE_BWD, OP_DESLICE_BWD, OP_STATS, OP_TIED_BWD = range(6)
 
 _DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
 #: every entry point the header declares
 EXPORTS = ("fs_workspace_bytes", "fs_compute_stats", "fs_slice_fwd", "fs_deslice_fwd",
-           "fs_slice_bwd", "fs_deslice_bwd", "fs_family", "fs_last_error", "fs_version",
+           "fs_slice_bwd", "fs_deslice_bwd", "fs_tied_bwd", "fs_family", "fs_last_error",
+           "fs_version",
            # the layer around the path (include/flashslice_layer.h)
            "fs_layernorm_fwd", "fs_layernorm_bwd", "fs_layernorm_workspace_bytes")
 
@@ -63,8 +64,9 @@ def _declare(lib):
     lib.fs_deslice_fwd.argtypes = [pts, prm, V, V, V, pts, V, S, V]
     lib.fs_slice_bwd.argtypes = [pts, pts, prm, V, V, V, pts, pts, V, V, V, V, S, V]
     lib.fs_deslice_bwd.argtypes = [pts, prm, V, V, pts, pts, V, V, V, V, V, S, V]
+    lib.fs_tied_bwd.argtypes = [pts, pts, pts, prm, V, V, V, pts, pts, V, V, V, V, V, S, V]
     for name in ("fs_compute_stats", "fs_slice_fwd", "fs_deslice_fwd", "fs_slice_bwd",
-                 "fs_deslice_bwd"):
+                 "fs_deslice_bwd", "fs_tied_bwd"):
         getattr(lib, name).restype = I32
     lib.fs_family.argtypes = [prm]
     lib.fs_family.restype = I32

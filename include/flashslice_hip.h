@@ -53,7 +53,8 @@ enum fs_op {
   FS_OP_DESLICE_FWD = 1,
   FS_OP_SLICE_BWD = 2,
   FS_OP_DESLICE_BWD = 3,
-  FS_OP_STATS = 4
+  FS_OP_STATS = 4,
+  FS_OP_TIED_BWD = 5
 };
 
 /* A (B, N, H, width) tensor of points: x_mid, fx_mid, d_out, out, dx, dfx. */
@@ -119,6 +120,24 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
                        const float* stats_in, const fs_points* d_out, const fs_points* dx,
                        float* dtokens, float* dweight, float* dbias, float* dtau,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* Backward of a deslice -> slice coupling on one x_mid, weight, bias, tau
+ * (out = deslice(tokens), (z_num, s) = slice(fx_mid), fx_mid not computed
+ * from out) in one pass over the points: both ops' gradients from one
+ * recompute of the softmax weights, one softmax Jacobian and one dx. Writes
+ * dx (like x), dfx (like fx), dtokens (B, H, G, DV) fp32 and the summed
+ * dweight, dbias, dtau of both ops. It replaces the pair fs_deslice_bwd +
+ * fs_slice_bwd and autograd's sum of their two dx, i.e. the reference's
+ * _deslice_bwd_impl and _slice_bwd_impl (slice_ops.py:822-885) run back to
+ * back on the same saved inputs; it is the "tied backward fusion" of the
+ * reference's ROADMAP.md:58-65, which the reference does not implement.
+ * Served by the whole-G family only (fs_family() == 1); other shapes return
+ * FS_ERR_UNSUPPORTED and the caller runs the two backward ops. */
+int32_t fs_tied_bwd(const fs_points* x, const fs_points* fx, const fs_points* d_out,
+                    const fs_slice_params* p, const float* tokens, const float* dz_num,
+                    const float* ds, const fs_points* dx, const fs_points* dfx,
+                    float* dtokens, float* dweight, float* dbias, float* dtau,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* Which kernel family serves this call: 1 = whole-G (the slot axis held in
  * registers, one pass per op; chosen where the shape fits, G <= 128 and

@@ -21,8 +21,8 @@ import math
 import torch
 
 import oracle
-from flashslice_amd.kernels import (fused_deslice, fused_slice, set_dot_mode,
-                                    set_kernel_mode)
+from flashslice_amd.kernels import (fused_deslice, fused_deslice_slice, fused_slice,
+                                    set_dot_mode, set_kernel_mode)
 
 
 def relerr(a, ref):
@@ -87,13 +87,16 @@ class Case:
                 z, s, st = fused_slice(x, fx, w, b, tau, return_stats=True)
                 tk = (z / (s + oracle.EPS_TOKEN)[..., None]) @ tm.float()
                 out = fused_deslice(x, w, b, tau, tk, stats=st)
+            elif order == "tied":  # deslice-first as one op with one backward pass
+                out, z, s = fused_deslice_slice(x, fx, w, b, tau, tok.float())
             else:
                 out, st = fused_deslice(x, w, b, tau, tok.float(), return_stats=True)
                 z, s = fused_slice(x, fx, w, b, tau, stats=st)
         else:
             f32 = (lambda t: None if t is None else (t.float() if amp else t))  # noqa: E731
             out, z, s = oracle.coupling(f32(x), f32(fx), f32(w), f32(b), tau, tm=tm,
-                                        tokens=tok, order=order)
+                                        tokens=tok,
+                                        order="deslice-first" if order == "tied" else order)
         res = {"out": out.detach(), "z_num": z.detach(), "s": s.detach()}
         if grads:
             up = {k: v.to(device) for k, v in self.up.items()}
