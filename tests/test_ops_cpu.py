@@ -135,3 +135,70 @@ def test_compile_keeps_one_graph():
                                               t["b"], t["tau"])
     assert explain.graph_break_count == 0, explain.break_reasons
     assert explain.graph_count == 1
+
+
+# ---------------------------------------------------------------- tied op
+TIED_SCHEMAS = {
+    "deslice_slice": "deslice_slice(Tensor x_mid, Tensor fx_mid, Tensor weight, Tensor bias, "
+                     "Tensor tau, Tensor tokens, int dot) -> (Tensor, Tensor, Tensor)",
+    "deslice_slice_bwd": "deslice_slice_bwd(Tensor x_mid, Tensor fx_mid, Tensor weight, "
+                         "Tensor bias, Tensor tau, Tensor tokens, Tensor d_out, Tensor dz_num, "
+                         "Tensor ds, int dot) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)",
+}
+
+
+@pytest.mark.parametrize("name", sorted(TIED_SCHEMAS))
+def test_tied_schema(name):
+    op = getattr(torch.ops.flashslice, name).default
+    assert _norm(str(op._schema)) == _norm(TIED_SCHEMAS[name])
+
+
+def test_tied_fakes_and_autograd():
+    """fused_deslice_slice: (out, z_num, s) with the two ops' shapes and
+    dtypes; its backward node gives every input's gradient in that input's
+    shape and dtype (meta tensors: the fakes only)."""
+    from flashslice_amd.kernels import fused_deslice_slice
+    B, N, H, D, DV, G = 2, 37, 3, 8, 12, 5
+    m = lambda *s, dtype=torch.float32: torch.empty(  # noqa: E731
+        *s, device="meta", dtype=dtype, requires_grad=True)
+    x, fx = m(B, N, H, D, dtype=torch.bfloat16), m(B, N, H, DV, dtype=torch.bfloat16)
+    w, b, tau, tok = m(B, H, G, D), m(H, G), m(H), m(B, H, G, DV)
+    out, z, s = fused_deslice_slice(x, fx, w, b, tau, tok)
+    assert out.shape == (B, N, H, DV) and out.dtype == torch.bfloat16
+    assert z.shape == (B, H, G, DV) and z.dtype == torch.float32
+    assert s.shape == (B, H, G) and s.dtype == torch.float32
+    gs = torch.autograd.grad(out.float().sum() + z.sum() + s.sum(), [x, fx, w, b, tau, tok])
+    assert [g.shape for g in gs] == [t.shape for t in (x, fx, w, b, tau, tok)]
+    assert [g.dtype for g in gs] == [t.dtype for t in (x, fx, w, b, tau, tok)]
+    # only some outputs used: the others' gradients are taken as zeros
+    out, z, s = fused_deslice_slice(x, fx, w, b, tau, tok)
+    gs = torch.autograd.grad(s.sum(), [x, w])
+    assert gs[0].shape == x.shape
+
+
+def test_tied_errors_and_no_cpu_fallback():
+    from flashslice_amd.kernels import fused_deslice_slice
+    x = torch.randn(1, 8, 2, 4)
+    w, b, tau = torch.randn(3, 4), torch.zeros(3), torch.ones(2)
+    with pytest.raises(ValueError, match="tokens have width 5, fx_mid 4"):
+        fused_deslice_slice(x, x, w, b, tau, torch.randn(1, 2, 3, 5))
+    with pytest.raises(ValueError, match="weight's last dim"):
+        fused_deslice_slice(x, x, torch.randn(3, 5), b, tau, torch.randn(1, 2, 3, 4))
+    with pytest.raises(NotImplementedError):
+        fused_deslice_slice(x, x, w, b, tau, torch.randn(1, 2, 3, 4))
+
+
+def test_tied_compile_keeps_one_graph():
+    import torch._dynamo
+    from flashslice_amd.kernels import fused_deslice_slice
+
+    def stream(x, fx, w, b, tau, tok):
+        out, z, s = fused_deslice_slice(x, fx, w, b, tau, tok)
+        return out, z / (s + 1e-5)[..., None]
+
+    torch._dynamo.reset()
+    m = lambda *s: torch.empty(*s, device="meta")  # noqa: E731
+    explain = torch._dynamo.explain(stream)(m(2, 37, 3, 8), m(2, 37, 3, 8), m(3, 5, 8), m(3, 5),
+                                            m(3), m(2, 3, 5, 8))
+    assert explain.graph_break_count == 0, explain.break_reasons
+    assert explain.graph_count == 1
