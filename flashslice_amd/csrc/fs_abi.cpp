@@ -206,7 +206,28 @@ fs::Args base_args(const fs_slice_params* p, const Geo& g) {
   a.ntiles = g.ntiles;
   a.nd = (int)((p->D + 31) / 32);
   a.nv = (int)((p->DV + 31) / 32);
+  a.rows = p->row_splits;
   return a;
+}
+
+// A ragged batch addresses sample b from its first row (row splits): the
+// point tensors' strides along b are not used.
+void ragged_strides(fs::Args& a) {
+  if (!a.rows) return;
+  a.sxb = a.sfb = a.s1b = a.s2b = a.sgb = 0;
+}
+
+// Row splits need the whole-G kernels and no statistics.
+int32_t check_rows(const fs_slice_params* p, const void* stats_in, const void* stats_out,
+                   const char* who) {
+  if (!p->row_splits) return FS_OK;
+  if (family_of(p) != 1)
+    return fail(FS_ERR_UNSUPPORTED,
+                "%s: row splits are served by the whole-G kernels only (G <= 128 and D, DV "
+                "small enough, family not forced to 2)", who);
+  if (stats_in || stats_out)
+    return fail(FS_ERR_UNSUPPORTED, "%s: statistics are not supported with row splits", who);
+  return FS_OK;
 }
 
 void set_in(const fs_points* t, const void** d, int64_t* sb, int64_t* sn, int64_t* sh) {
@@ -366,6 +387,8 @@ int32_t fs_compute_stats(const fs_points* x, const fs_slice_params* p, float* st
   int32_t rc = check_params(p, who);
   if (!rc) rc = check_points(x, "x_mid", p->D, who);
   if (rc) return rc;
+  if (p->row_splits)
+    return fail(FS_ERR_UNSUPPORTED, "%s: statistics are not supported with row splits", who);
   if (!stats) return fail(FS_ERR_INVALID, "%s: stats is NULL", who);
   const Workspace ws = plan_ws(FS_OP_STATS, p, (char*)workspace);
   rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
@@ -387,6 +410,8 @@ int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_par
   if (rc) return rc;
   if (fx->dtype != x->dtype) return fail(FS_ERR_INVALID, "%s: x_mid and fx_mid dtypes differ", who);
   if (!z_num || !s) return fail(FS_ERR_INVALID, "%s: z_num and s must be non-NULL", who);
+  rc = check_rows(p, stats_in, stats_out, who);
+  if (rc) return rc;
   const Workspace ws = plan_ws(FS_OP_SLICE_FWD, p, (char*)workspace);
   rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
   if (rc) return rc;
@@ -407,6 +432,7 @@ int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     a.fast = a.vec_x && a.vec_f && full_widths(p);
     a.part = ws.part;
     a.stats_out = stats_out;
+    ragged_strides(a);
     rc = hip_check(fs::launch_fused_slice_fwd(a, x->dtype, mode, st), who);
   } else {
     g = geo_g(p, mode);
@@ -449,6 +475,8 @@ int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float
   if (rc) return rc;
   if (out->dtype != x->dtype) return fail(FS_ERR_INVALID, "%s: out and x_mid dtypes differ", who);
   if (!tokens) return fail(FS_ERR_INVALID, "%s: tokens is NULL", who);
+  rc = check_rows(p, stats_in, stats_out, who);
+  if (rc) return rc;
   const Workspace ws = plan_ws(FS_OP_DESLICE_FWD, p, (char*)workspace);
   rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
   if (rc) return rc;
@@ -464,6 +492,7 @@ int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float
     a.fast = a.vec_x && a.vec_1 && full_widths(p);
     a.tok = tokens;
     a.stats_out = stats_out;
+    ragged_strides(a);
     return hip_check(fs::launch_fused_deslice_fwd(a, x->dtype, mode, st), who);
   }
   const Geo g = geo_gp(p, GPG_DESLICE, mode);
@@ -499,6 +528,8 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     return fail(FS_ERR_INVALID, "%s: point tensors must share one dtype", who);
   if (!dz_num || !ds || !dweight || !dbias || !dtau)
     return fail(FS_ERR_INVALID, "%s: dz_num, ds, dweight, dbias, dtau must be non-NULL", who);
+  rc = check_rows(p, stats_in, nullptr, who);
+  if (rc) return rc;
   const Workspace ws = plan_ws(FS_OP_SLICE_BWD, p, (char*)workspace);
   rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
   if (rc) return rc;
@@ -524,6 +555,7 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     a.tok = dz_num;
     a.ds = ds;
     a.part = ws.part;
+    ragged_strides(a);
     rc = hip_check(fs::launch_fused_slice_bwd(a, x->dtype, mode, st), who);
     if (rc) return rc;
     rs.seg[0] = seg(ws.part, wf, 0, pb(g), G * D, Bw, Hw, dweight);
@@ -584,6 +616,8 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
   if (!tokens || !dtokens || !dweight || !dbias || !dtau)
     return fail(FS_ERR_INVALID, "%s: tokens, dtokens, dweight, dbias, dtau must be non-NULL",
                 who);
+  rc = check_rows(p, stats_in, nullptr, who);
+  if (rc) return rc;
   const Workspace ws = plan_ws(FS_OP_DESLICE_BWD, p, (char*)workspace);
   rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
   if (rc) return rc;
@@ -607,6 +641,7 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
     a.fast = a.vec_x && a.vec_f && a.vec_1 && full_widths(p);
     a.tok = tokens;
     a.part = ws.part;
+    ragged_strides(a);
     rc = hip_check(fs::launch_fused_deslice_bwd(a, x->dtype, mode, st), who);
     if (rc) return rc;
     rs.seg[0] = seg(ws.part, wf, 0, pb(g), G * DV, (int)p->B, (int)p->H, dtokens);
@@ -674,6 +709,8 @@ int32_t fs_tied_bwd(const fs_points* x, const fs_points* fx, const fs_points* d_
     return fail(FS_ERR_UNSUPPORTED,
                 "%s: served by the whole-G kernels only (G <= 128 and D, DV small enough); "
                 "run fs_deslice_bwd and fs_slice_bwd", who);
+  rc = check_rows(p, nullptr, nullptr, who);
+  if (rc) return rc;
   const Workspace ws = plan_ws(FS_OP_TIED_BWD, p, (char*)workspace);
   rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
   if (rc) return rc;
@@ -700,6 +737,7 @@ int32_t fs_tied_bwd(const fs_points* x, const fs_points* fx, const fs_points* d_
   a.tok2 = tokens;
   a.ds = ds;
   a.part = ws.part;
+  ragged_strides(a);
   rc = hip_check(fs::launch_fused_tied_bwd(a, x->dtype, mode, st), who);
   if (rc) return rc;
   fs::ReduceSegments rs{};

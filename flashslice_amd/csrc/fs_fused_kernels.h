@@ -108,7 +108,11 @@ __device__ __forceinline__ void acc_put(float& t, float v, bool first) { t = fir
   const int bh = blockIdx.y;                                                        \
   const int b = bh / a.H, hd = bh - b * a.H;                                       \
   const int pid = blockIdx.x * kWavesPerBlock + wid;                                \
-  const int G = a.G, D = a.D, DV = a.DV, N = a.N;                                   \
+  /* row splits (ragged batch): sample b is rows rows[b] .. rows[b + 1] - 1 */      \
+  const int64_t row0_ = a.rows ? a.rows[b] : 0;                                     \
+  const int G = a.G, D = a.D, DV = a.DV;                                            \
+  const int N = a.rows ? (int)(a.rows[b + 1] - row0_) : a.N;                        \
+  const int ntiles_ = a.rows ? (N + kTile - 1) / kTile : a.ntiles;                  \
   float* sW = smem;                                                                 \
   float* sV = smem + SM::GP * SM::SW;                                               \
   float* lds = smem + wid * (WF);                                                   \
@@ -152,10 +156,12 @@ __device__ __forceinline__ void acc_put(float& t, float v, bool first) { t = fir
   }
 
 // Point slices of one (b, h): byte base, byte row stride and row width in
-// bytes of a (B, N, H, C) tensor with element strides (sb, sn, sh), and the
-// byte offset of this lane's row c inside a tile.
+// bytes of a (B, N, H, C) tensor with element strides (sb, sn, sh) -- of a
+// (1, rows, H, C) tensor from row row0_ on with row splits (sb = 0) -- and
+// the byte offset of this lane's row c inside a tile.
 #define FS_SLICE(NAME, PTR, SB, SN, SH, C)                                                \
-  const char* NAME##_b = (const char*)(PTR) + (b * (SB) + hd * (SH)) * (int64_t)sizeof(T); \
+  const char* NAME##_b =                                                                  \
+      (const char*)(PTR) + (b * (SB) + row0_ * (SN) + hd * (SH)) * (int64_t)sizeof(T);    \
   const int64_t NAME##_sn = (SN) * (int64_t)sizeof(T);                                    \
   const int64_t NAME##_w = (int64_t)(C) * (int64_t)sizeof(T);                             \
   const uint32_t NAME##_row = (uint32_t)(c * NAME##_sn);

@@ -155,8 +155,9 @@ __device__ __forceinline__ void gp_vec(float (&v)[16], const u32x4* item, int la
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);               \
   const int c = lane & 31, h = lane >> 5;                                         \
   const int G = a.G, D = a.D, DV = a.DV, N = a.N, nd = a.nd, nv = a.nv;           \
+  const int ntiles_ = a.ntiles;                                                   \
   const int ngb = (G + 31) / 32;                                                  \
-  (void)D; (void)DV; (void)nd; (void)nv;
+  (void)D; (void)DV; (void)nd; (void)nv; (void)ntiles_;
 
 #define GP_HEAD(BH)                                                               \
   const int bh = (BH);                                                            \

@@ -31,6 +31,8 @@ struct Args {
   float* lsum;                             // (B, H, N) row sums formed by the point-owned bwd pass
   float* part;                             // per-wave partials (workspace)
   float* part2;                            // per-wave dtau partials of point-owned kernels
+  const int64_t* rows;                     // row splits (B + 1) of a ragged batch, or null
+                                           // (whole-G family; point strides along b are 0)
   int B, N, H, D, DV, G;
   int P;                                   // point partitions per (b, h), a multiple of 4
   int ntiles;                              // ceil(N / 32)

@@ -243,26 +243,27 @@ __device__ __forceinline__ void balance_prio(int t, int pid, int ntiles, int P) 
 // pass is peeled so that the loop is entered with the same memory operations
 // outstanding as on every back edge: the compiler then waits only for the
 // rows a tile needs, never for the stores still in flight. A load beyond the
-// last tile reads an empty range (zeros, no memory traffic).
+// last tile reads an empty range (zeros, no memory traffic). The caller's
+// scope defines ntiles_, the tiles of its (b, h).
 #define FS_TILE_LOOP(LOAD, BODY, BAL, A_ARGS, B_ARGS)                                     \
   {                                                                                       \
     int t_ = pid;                                                                         \
     LOAD(A_ARGS, t_);                                                                     \
     LOAD(B_ARGS, t_ + a.P);                                                               \
-    if (t_ < a.ntiles) {                                                                  \
+    if (t_ < ntiles_) {                                                                  \
       BODY(A_ARGS, t_, TileEven());                                                       \
       LOAD(A_ARGS, t_ + 2 * a.P);                                                         \
-      if constexpr (BAL) balance_prio(t_, pid, a.ntiles, a.P);                            \
+      if constexpr (BAL) balance_prio(t_, pid, ntiles_, a.P);                            \
       t_ += a.P;                                                                          \
-      while (t_ < a.ntiles) {                                                             \
+      while (t_ < ntiles_) {                                                             \
         BODY(B_ARGS, t_, TileOdd());                                                      \
         LOAD(B_ARGS, t_ + 2 * a.P);                                                       \
-        if constexpr (BAL) balance_prio(t_, pid, a.ntiles, a.P);                          \
+        if constexpr (BAL) balance_prio(t_, pid, ntiles_, a.P);                          \
         t_ += a.P;                                                                        \
-        if (t_ >= a.ntiles) break;                                                        \
+        if (t_ >= ntiles_) break;                                                        \
         BODY(A_ARGS, t_, TileEven());                                                     \
         LOAD(A_ARGS, t_ + 2 * a.P);                                                       \
-        if constexpr (BAL) balance_prio(t_, pid, a.ntiles, a.P);                          \
+        if constexpr (BAL) balance_prio(t_, pid, ntiles_, a.P);                          \
         t_ += a.P;                                                                        \
       }                                                                                   \
     }                                                                                     \

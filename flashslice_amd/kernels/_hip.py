@@ -43,7 +43,8 @@ class FsSliceParams(ctypes.Structure):
                 ("bias", ctypes.c_void_p),
                 ("b_stride_b", ctypes.c_int64), ("b_stride_h", ctypes.c_int64),
                 ("tau", ctypes.c_void_p),
-                ("dot", ctypes.c_int32), ("family", ctypes.c_int32)]
+                ("dot", ctypes.c_int32), ("family", ctypes.c_int32),
+                ("row_splits", ctypes.c_void_p)]
 
 
 class FlashSliceLibError(RuntimeError):
@@ -113,7 +114,9 @@ def dtype_code(t):
 
 
 def points(t, width):
-    """FsPoints of a (B, N, H, width) tensor with unit stride on the last dim."""
+    """FsPoints of a (B, N, H, width) tensor with unit stride on the last dim
+    (a (1, rows, H, width) view of a ragged batch's points: its stride along
+    b is not used)."""
     assert t.dim() == 4 and t.stride(3) == 1 and t.dtype in _DTYPES
     return FsPoints(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2), _DTYPES[t.dtype], width)
 

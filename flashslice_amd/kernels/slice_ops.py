@@ -253,8 +253,13 @@ class _Call:
     """The fp32 small operands and the FsSliceParams of one call (holding
     references so the converted tensors outlive the launch)."""
 
-    def __init__(self, x_mid, weight, bias, tau, dv, dot):
+    def __init__(self, x_mid, weight, bias, tau, dv, dot, rows=None):
         B, N, H, D = x_mid.shape
+        if rows is not None:
+            # ragged batch (varlen.py): x_mid is the (1, rows, H, D) view of the
+            # concatenated samples; rows = (row splits on the device, samples,
+            # longest sample)
+            B, N = rows[1], rows[2]
         self.device = x_mid.device
         self.weight = weight.detach().to(torch.float32).contiguous()
         self.bias = bias.detach().to(torch.float32).contiguous()
@@ -269,7 +274,9 @@ class _Call:
         self.prm = _hip.FsSliceParams(B, N, H, D, dv, G,
                                       self.weight.data_ptr(), swb, swh,
                                       self.bias.data_ptr(), sbb, sbh,
-                                      self.tau.data_ptr(), int(dot), family)
+                                      self.tau.data_ptr(), int(dot), family,
+                                      None if rows is None else rows[0].data_ptr())
+        self.rows = rows  # keeps the row splits alive across the launch
         self.B, self.N, self.H, self.D, self.DV, self.G = B, N, H, D, dv, G
 
     def workspace(self, op):
@@ -287,11 +294,13 @@ def _small(t):
     return t.detach().to(torch.float32).contiguous()
 
 
-def _hip_slice_fwd(x_mid, fx_mid, weight, bias, tau, dot, stats_in=None, want_stats=False):
+def _hip_slice_fwd(x_mid, fx_mid, weight, bias, tau, dot, stats_in=None, want_stats=False,
+                   rows=None):
     B, N, H, D = x_mid.shape
     DV = fx_mid.shape[3]
     with torch.cuda.device(x_mid.device):
-        call = _Call(x_mid, weight, bias, tau, DV, dot)
+        call = _Call(x_mid, weight, bias, tau, DV, dot, rows)
+        B = call.B
         dt = _point_dtype(x_mid, fx_mid)
         x, fx = _as_points(x_mid, dt), _as_points(fx_mid, dt)
         z_num = torch.empty(B, H, call.G, DV, device=x.device, dtype=torch.float32)
@@ -306,11 +315,12 @@ def _hip_slice_fwd(x_mid, fx_mid, weight, bias, tau, dot, stats_in=None, want_st
     return z_num, s, (st_in if st_in is not None else st_out)
 
 
-def _hip_deslice_fwd(x_mid, weight, bias, tau, tokens, dot, stats_in=None, want_stats=False):
+def _hip_deslice_fwd(x_mid, weight, bias, tau, tokens, dot, stats_in=None, want_stats=False,
+                     rows=None):
     B, N, H, D = x_mid.shape
     DV = tokens.shape[3]
     with torch.cuda.device(x_mid.device):
-        call = _Call(x_mid, weight, bias, tau, DV, dot)
+        call = _Call(x_mid, weight, bias, tau, DV, dot, rows)
         dt = _point_dtype(x_mid)
         x = _as_points(x_mid, dt)
         tok = _small(tokens)
@@ -345,11 +355,12 @@ def _param_grad_buffers(call):
     return dW, db, dtau
 
 
-def _hip_slice_bwd(x_mid, fx_mid, weight, bias, tau, dz_num, ds, dot, stats_in=None):
+def _hip_slice_bwd(x_mid, fx_mid, weight, bias, tau, dz_num, ds, dot, stats_in=None,
+                   rows=None):
     B, N, H, D = x_mid.shape
     DV = fx_mid.shape[3]
     with torch.cuda.device(x_mid.device):
-        call = _Call(x_mid, weight, bias, tau, DV, dot)
+        call = _Call(x_mid, weight, bias, tau, DV, dot, rows)
         dt = _point_dtype(x_mid, fx_mid)
         x, fx = _as_points(x_mid, dt), _as_points(fx_mid, dt)
         dxm = torch.empty_like(x_mid, dtype=dt) if x_mid.stride(3) == 1 else \
@@ -371,11 +382,13 @@ def _hip_slice_bwd(x_mid, fx_mid, weight, bias, tau, dz_num, ds, dot, stats_in=N
     return (dxm, dfx) + _grads_out(call, weight, bias, tau, dW, db, dtau)
 
 
-def _hip_deslice_bwd(x_mid, weight, bias, tau, tokens, d_out, dot, stats_in=None):
+def _hip_deslice_bwd(x_mid, weight, bias, tau, tokens, d_out, dot, stats_in=None,
+                     rows=None):
     B, N, H, D = x_mid.shape
     DV = tokens.shape[3]
     with torch.cuda.device(x_mid.device):
-        call = _Call(x_mid, weight, bias, tau, DV, dot)
+        call = _Call(x_mid, weight, bias, tau, DV, dot, rows)
+        B = call.B
         dt = _point_dtype(x_mid, d_out)
         x, do = _as_points(x_mid, dt), _as_points(d_out, dt)
         dxm = torch.empty_like(x_mid, dtype=dt) if x_mid.stride(3) == 1 else \

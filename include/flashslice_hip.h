@@ -75,6 +75,15 @@ typedef struct fs_slice_params {
   const float* tau;                     /* (H,) fp32 */
   int32_t dot;                          /* 0 ieee, 1 tf32, 2 bf16v, 3 bf16, 4 tf32x3 */
   int32_t family;                       /* 0 auto, 1 whole-G where it fits, 2 G-blocked */
+  /* Ragged batch (NULL = none): B samples of different lengths concatenated
+   * along the point axis; sample b is rows row_splits[b] .. row_splits[b+1]-1
+   * of every point tensor, whose stride_b is then ignored. Device memory,
+   * B + 1 non-decreasing int64 with row_splits[0] = 0 and no sample longer
+   * than N (N sizes the launch; it is not read from the device). Served by
+   * the whole-G family only, without statistics (stats_in / stats_out must
+   * be NULL; fs_compute_stats refuses it): FS_ERR_UNSUPPORTED otherwise.
+   * No counterpart in the reference, whose ROADMAP.md:66-68 plans it. */
+  const int64_t* row_splits;
 } fs_slice_params;
 
 /* Bytes of workspace an op needs for this shape (op: enum fs_op). */

@@ -202,3 +202,36 @@ def test_tied_compile_keeps_one_graph():
                                             m(3), m(2, 3, 5, 8))
     assert explain.graph_break_count == 0, explain.break_reasons
     assert explain.graph_count == 1
+
+
+# ------------------------------------------------------------ ragged batches
+def test_varlen_fakes_autograd_and_validation():
+    """fused_slice_varlen / fused_deslice_varlen: per-sample slot sums
+    (B, H, G, DV), per-row outputs (rows, H, DV); every input's gradient in
+    its own shape; row splits validated on the host."""
+    from flashslice_amd.kernels import fused_deslice_varlen, fused_slice_varlen
+    m = lambda *s: torch.empty(*s, device="meta", requires_grad=True)  # noqa: E731
+    x, fx, W, b, tau, tok = m(100, 4, 32), m(100, 4, 64), m(3, 4, 64, 32), m(4, 64), m(4), \
+        m(3, 4, 64, 64)
+    rs = [0, 40, 40, 100]  # the middle sample is empty
+    z, s = fused_slice_varlen(x, fx, W, b, tau, rs)
+    assert z.shape == (3, 4, 64, 64) and s.shape == (3, 4, 64) and z.dtype == torch.float32
+    out = fused_deslice_varlen(x, W, b, tau, tok, rs)
+    assert out.shape == (100, 4, 64)
+    gs = torch.autograd.grad(z.sum() + s.sum() + out.sum(), [x, fx, W, b, tau, tok])
+    assert [g.shape for g in gs] == [t.shape for t in (x, fx, W, b, tau, tok)]
+    for bad, msg in (([0, 40, 30, 100], "rise from 0"), ([1, 40, 100], "rise from 0"),
+                     ([0, 40, 99], "rise from 0"), ([0], "B \\+ 1 offsets")):
+        with pytest.raises(ValueError, match=msg):
+            fused_slice_varlen(x, fx, W, b, tau, bad)
+    with pytest.raises(ValueError, match="max_rows=10 is below"):
+        fused_slice_varlen(x, fx, W, b, tau, rs, max_rows=10)
+    with pytest.raises(ValueError, match="weight has 3 along batch"):
+        fused_slice_varlen(x, fx, W, b, tau, [0, 50, 100])
+    with pytest.raises(ValueError, match="tokens must be"):
+        fused_deslice_varlen(x, W, b, tau, m(2, 4, 64, 64), rs)
+    with pytest.raises(ValueError, match="rows, H, D"):
+        fused_slice_varlen(m(1, 100, 4, 32), fx, W, b, tau, rs)
+    with pytest.raises(NotImplementedError):  # no CPU fallback
+        fused_slice_varlen(torch.randn(10, 2, 4), torch.randn(10, 2, 4), torch.randn(3, 4),
+                           None, torch.ones(2), [0, 4, 10])
