@@ -453,7 +453,8 @@ def main():
     total_bytes = sum(bytes_[n] for n in OPS)
     total_flops = sum(flops[n] for n in OPS)
     step_ach = total_bytes / (ms_step * 1e-3) / 1e9
-    traffic = measured_traffic(a.workload)
+    traffic_name = a.workload + ("-tied" if a.tied else "")
+    traffic = measured_traffic(traffic_name)
 
     cpu = None
     if not a.no_cpu_baseline:
@@ -482,7 +483,7 @@ def main():
                      {"bound": "mfma", "kernel": dom, "achieved": round(ach_tf, 2),
                       "peak": MFMA_PEAK_TFLOPS[a.dot], "unit": "TFLOP/s",
                       "frac": round(ach_tf / MFMA_PEAK_TFLOPS[a.dot], 4)}),
-        "traffic_source": ("profiles/%s_hbm_traffic.txt" % a.workload) if traffic else None,
+        "traffic_source": ("profiles/%s_hbm_traffic.txt" % traffic_name) if traffic else None,
         "step_roofline": {"alg_bytes": total_bytes, "achieved_GBs": round(step_ach, 1),
                           "hbm_frac": round(step_ach / HBM_PEAK_GBS, 4),
                           "alg_flops": total_flops,
@@ -494,7 +495,7 @@ def main():
         "cpu_baseline": cpu,
     }
     line["roofline"].update({
-        "traffic": traffic.get(dom) if traffic and not a.tied else None,
+        "traffic": traffic.get(dom) if traffic else None,
         "alg_bytes_per_launch": bytes_[dom], "alg_flops_per_launch": flops[dom],
         "ms_per_launch": round(per_op[dom], 4)})
     print(json.dumps(line), flush=True)
