@@ -1,6 +1,7 @@
 """Benchmark of the fused slice/deslice hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3-256|c3-1024|c4]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload c2|c3-256|c3-1024|c4|c5|ragged] [--tied]
 
 One step is the coupling the metric names ("slice+deslice
 fwd+bwd ms & Mpoints/s at N=1M, H=8, D=32, G=32; peak HBM"): the four
@@ -66,6 +67,14 @@ MODEL_WORKLOADS = {
                n_layers=8, slice_num=32,
                desc="C5: Transolver fwd+bwd (MSE), B=1 N=2e6, n_hidden=256, 8 heads, 8 layers, "
                     "G=32, fp32, use_fused_slice=True"),
+}
+# ragged batch (reference ROADMAP.md:66-68): many small meshes of different N
+# in one launch through row splits, against the per-sample loop it replaces
+RAGGED_WORKLOADS = {
+    "ragged": dict(B=64, n_min=2_000, n_max=40_000, H=8, D=32, DV=32, G=32,
+                   desc="ragged: 64 meshes of N ~ U[2000, 40000] (1.34M points), H=8 "
+                        "D=DV=G=32 fp32 ieee, per-head W, slice->deslice fwd+bwd in one "
+                        "launch per op through row splits"),
 }
 # dot level per run (reference slice_ops.py:336-343): 0 ieee; 3 bf16 (bf16 inputs)
 DOTS = {"ieee": 0, "bf16": 3}
@@ -231,6 +240,89 @@ def cpu_baseline(B, N, H, D, DV, G, layout, order, budget_s=20.0):
     return B * n / ts[1], n, torch.get_num_threads()
 
 
+def bench_ragged(a, cfg):
+    """One step = the slice -> deslice coupling of every mesh, forward and
+    backward (the four ops of the C2 step), as ONE launch per op through row
+    splits (``flashslice::*_varlen``); beside it the same work as a loop of
+    per-mesh calls of the regular ops (B = 1 each), the fixed per-call floor
+    that ragged batching removes. Inputs as C2's, per mesh."""
+    ops = torch.ops.flashslice
+    g = torch.Generator().manual_seed(0)
+    B, H, D, DV, G = cfg["B"], cfg["H"], cfg["D"], cfg["DV"], cfg["G"]
+    lens = torch.randint(cfg["n_min"], cfg["n_max"] + 1, (B,), generator=g).tolist()
+    rows = sum(lens)
+    splits = [0]
+    for n in lens:
+        splits.append(splits[-1] + n)
+    dev = torch.device("cuda:0")
+    x, fx, W, b, tau, d_out, dzb, dsb, _ = make_inputs(1, rows, H, D, DV, G, "hgd", dev)
+    x, fx, d_out = x[0], fx[0], d_out[0]
+    dzb = torch.randn(B, H, G, DV, generator=g).to(dev)
+    dsb = torch.randn(B, H, G, generator=g).to(dev)
+    rs = torch.tensor(splits, dtype=torch.int64, device=dev)
+    nmax = max(lens)
+
+    def ragged():
+        z, s = ops.slice_varlen(x, fx, W, b, tau, rs, nmax, 0)
+        den = (s + EPS)[..., None]
+        tok = z / den
+        out = ops.deslice_varlen(x, W, b, tau, tok, rs, nmax, 0)
+        dx1, dtok, dW1, db1, dt1 = ops.deslice_varlen_bwd(x, W, b, tau, tok, rs, nmax, d_out, 0)
+        dz = dzb + dtok / den
+        ds = dsb - (dtok * tok).sum(-1) / den[..., 0]
+        dx2, dfx, dW2, db2, dt2 = ops.slice_varlen_bwd(x, fx, W, b, tau, rs, nmax, dz, ds, 0)
+        return z, s, out, dx1, dtok, dx2, dfx
+
+    def looped():
+        res = []
+        for i in range(B):
+            sl = slice(splits[i], splits[i + 1])
+            xi, fi, oi = x[sl][None], fx[sl][None], d_out[sl][None]
+            z, s = ops.flash_slice(xi, fi, W, b, tau, 0)
+            den = (s + EPS)[..., None]
+            tok = z / den
+            out = ops.flash_deslice(xi, W, b, tau, tok, 0)
+            dx1, dtok, dW1, db1, dt1 = ops.flash_deslice_bwd(xi, W, b, tau, tok, oi, 0)
+            dz = dzb[i:i + 1] + dtok / den
+            ds = dsb[i:i + 1] - (dtok * tok).sum(-1) / den[..., 0]
+            res.append(ops.flash_slice_bwd(xi, fi, W, b, tau, dz, ds, 0))
+        return res
+
+    def timed(fn, k):
+        for _ in range(a.warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(k):
+            fn()
+        torch.cuda.synchronize()
+        return 1e3 * (time.perf_counter() - t0) / k
+
+    r1 = [t.clone() for t in ragged()]
+    deterministic = all(torch.equal(u, v) for u, v in zip(r1, ragged()))
+    del r1
+    ms = timed(ragged, a.steps)
+    ms_loop = timed(looped, max(1, a.steps // 5))
+    nbytes = rows * H * (6 * D + 5 * DV) * 4
+    ach = nbytes / (ms * 1e-3) / 1e9
+    line = {
+        "metric": "ragged slice+deslice fwd+bwd Mpoints/s", "value": round(rows / (ms * 1e-3) / 1e6, 3),
+        "unit": "Mpoints/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": cfg["desc"], "samples": B, "rows": rows, "min_n": min(lens),
+                   "max_n": nmax, "H": H, "D": D, "DV": DV, "G": G},
+        "roofline": {"bound": "hbm", "kernel": "step (4 ops)", "achieved": round(ach, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                     "traffic": None, "alg_bytes_per_step": nbytes},
+        "per_sample_loop": {"ms_per_step": round(ms_loop, 4),
+                            "Mpoints_per_s": round(rows / (ms_loop * 1e-3) / 1e6, 3),
+                            "launches_per_step": 4 * B},
+        "deterministic": deterministic, "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def model_inputs(cfg, N, device, seed=0):
     """Coordinates uniform in the unit cube, per-point inputs and MSE targets
     ~N(0, 1), generated on the CPU from one seed."""
@@ -357,7 +449,8 @@ def main():
                     help="timed steps (default 50; 5 for the model workload)")
     ap.add_argument("--warmup", type=int, default=None,
                     help="untimed steps first (default 5; 2 for the model workload)")
-    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS) + sorted(MODEL_WORKLOADS))
+    ap.add_argument("--workload", default="c2",
+                    choices=sorted(WORKLOADS) + sorted(MODEL_WORKLOADS) + sorted(RAGGED_WORKLOADS))
     ap.add_argument("--dot", default="ieee", choices=sorted(DOTS),
                     help="dot level: ieee (fp32 inputs) or bf16 (x_mid, fx_mid, W in bf16)")
     ap.add_argument("--tied", action="store_true",
@@ -384,6 +477,9 @@ def main():
 
     if a.workload in MODEL_WORKLOADS:
         return bench_model(a, MODEL_WORKLOADS[a.workload])
+    if a.workload in RAGGED_WORKLOADS:
+        torch.cuda.set_device(0)
+        return bench_ragged(a, RAGGED_WORKLOADS[a.workload])
     B, N, H, D, DV, G, layout, order, desc = WORKLOADS[a.workload]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
