@@ -56,6 +56,11 @@ WORKLOADS = {
                "C3: slice->deslice fwd+bwd, B=1 N=1e6 H=8 D=DV=32 G=256 fp32 ieee, per-head W"),
     "c3-1024": (1, 1_000_000, 8, 32, 32, 1024, "hgd", "slice-first",
                 "C3: slice->deslice fwd+bwd, B=1 N=1e6 H=8 D=DV=32 G=1024 fp32 ieee, per-head W"),
+    # C2's shape in the persistent-stream order (deslice, then slice): where
+    # the tied backward (--tied) applies at this shape
+    "c2-df": (1, 1_000_000, 8, 32, 32, 32, "hgd", "deslice-first",
+              "C2 shape, deslice->slice fwd+bwd, B=1 N=1e6 H=8 D=DV=G=32 fp32 ieee, per-head W, "
+              "given tokens"),
     "c4": (4, 262_144, 8, 32, 64, 64, "bhgd", "deslice-first",
            "C4: deslice->slice fwd+bwd, B=4 N=262144 H=8 D=32 DV=64 G=64 fp32 ieee, "
            "per-sample W, given tokens"),
