@@ -289,9 +289,20 @@ class _Call:
         return _hip.stream_of(self.device)
 
 
-def _small(t):
-    """A small per-slot tensor (tokens, dz_num, ds, stats) as fp32 contiguous."""
+def _small(t, shape, name):
+    """A small per-slot tensor (tokens, dz_num, ds, stats) as fp32
+    contiguous, after checking its shape: the library reads it through a raw
+    pointer, so a wrong size must be refused before the launch."""
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError("%s has shape %s, expected %s" % (name, tuple(t.shape), tuple(shape)))
     return t.detach().to(torch.float32).contiguous()
+
+
+def _check_points(x_mid, t, width, name):
+    """A second point tensor of a call: x_mid's (B, N, H) and ``width``."""
+    if t.dim() != 4 or tuple(t.shape[:3]) != tuple(x_mid.shape[:3]) or t.shape[3] != width:
+        raise ValueError("%s has shape %s, expected %s" % (
+            name, tuple(t.shape), tuple(x_mid.shape[:3]) + (width,)))
 
 
 def _hip_slice_fwd(x_mid, fx_mid, weight, bias, tau, dot, stats_in=None, want_stats=False,
@@ -301,11 +312,12 @@ def _hip_slice_fwd(x_mid, fx_mid, weight, bias, tau, dot, stats_in=None, want_st
     with torch.cuda.device(x_mid.device):
         call = _Call(x_mid, weight, bias, tau, DV, dot, rows)
         B = call.B
+        _check_points(x_mid, fx_mid, DV, "fx_mid")
         dt = _point_dtype(x_mid, fx_mid)
         x, fx = _as_points(x_mid, dt), _as_points(fx_mid, dt)
         z_num = torch.empty(B, H, call.G, DV, device=x.device, dtype=torch.float32)
         s = torch.empty(B, H, call.G, device=x.device, dtype=torch.float32)
-        st_in = None if stats_in is None else _small(stats_in)
+        st_in = None if stats_in is None else _small(stats_in, (B, H, 2, N), "stats")
         st_out = (torch.empty(B, H, 2, N, device=x.device, dtype=torch.float32)
                   if want_stats and st_in is None else None)
         ws, nws = call.workspace(_hip.OP_SLICE_FWD)
@@ -323,9 +335,9 @@ def _hip_deslice_fwd(x_mid, weight, bias, tau, tokens, dot, stats_in=None, want_
         call = _Call(x_mid, weight, bias, tau, DV, dot, rows)
         dt = _point_dtype(x_mid)
         x = _as_points(x_mid, dt)
-        tok = _small(tokens)
+        tok = _small(tokens, (call.B, H, call.G, DV), "tokens")
         out = torch.empty(B, N, H, DV, device=x.device, dtype=dt)
-        st_in = None if stats_in is None else _small(stats_in)
+        st_in = None if stats_in is None else _small(stats_in, (B, H, 2, N), "stats")
         st_out = (torch.empty(B, H, 2, N, device=x.device, dtype=torch.float32)
                   if want_stats and st_in is None else None)
         ws, nws = call.workspace(_hip.OP_DESLICE_FWD)
@@ -361,14 +373,16 @@ def _hip_slice_bwd(x_mid, fx_mid, weight, bias, tau, dz_num, ds, dot, stats_in=N
     DV = fx_mid.shape[3]
     with torch.cuda.device(x_mid.device):
         call = _Call(x_mid, weight, bias, tau, DV, dot, rows)
+        _check_points(x_mid, fx_mid, DV, "fx_mid")
         dt = _point_dtype(x_mid, fx_mid)
         x, fx = _as_points(x_mid, dt), _as_points(fx_mid, dt)
         dxm = torch.empty_like(x_mid, dtype=dt) if x_mid.stride(3) == 1 else \
             torch.empty(x_mid.shape, device=x.device, dtype=dt)
         dfx = torch.empty_like(fx_mid, dtype=dt) if fx_mid.stride(3) == 1 else \
             torch.empty(fx_mid.shape, device=x.device, dtype=dt)
-        dz, dsv = _small(dz_num), _small(ds)
-        st_in = None if stats_in is None else _small(stats_in)
+        dz = _small(dz_num, (call.B, H, call.G, DV), "dz_num")
+        dsv = _small(ds, (call.B, H, call.G), "ds")
+        st_in = None if stats_in is None else _small(stats_in, (B, H, 2, N), "stats")
         dW, db, dtau = _param_grad_buffers(call)
         ws, nws = call.workspace(_hip.OP_SLICE_BWD)
         _hip.check(_hip.lib().fs_slice_bwd(
@@ -389,12 +403,13 @@ def _hip_deslice_bwd(x_mid, weight, bias, tau, tokens, d_out, dot, stats_in=None
     with torch.cuda.device(x_mid.device):
         call = _Call(x_mid, weight, bias, tau, DV, dot, rows)
         B = call.B
+        _check_points(x_mid, d_out, DV, "d_out")
         dt = _point_dtype(x_mid, d_out)
         x, do = _as_points(x_mid, dt), _as_points(d_out, dt)
         dxm = torch.empty_like(x_mid, dtype=dt) if x_mid.stride(3) == 1 else \
             torch.empty(x_mid.shape, device=x.device, dtype=dt)
-        tok = _small(tokens)
-        st_in = None if stats_in is None else _small(stats_in)
+        tok = _small(tokens, (B, H, call.G, DV), "tokens")
+        st_in = None if stats_in is None else _small(stats_in, (x_mid.shape[0], H, 2, N), "stats")
         dtok = torch.empty(B, H, call.G, DV, device=x.device, dtype=torch.float32)
         dW, db, dtau = _param_grad_buffers(call)
         ws, nws = call.workspace(_hip.OP_DESLICE_BWD)

@@ -31,7 +31,7 @@ import torch
 
 from . import _hip
 from .slice_ops import (
-    _Call, _LIB, _as_points, _check_dims, _dot_mode, _grads_out, _hip_deslice_bwd,
+    _Call, _LIB, _as_points, _check_dims, _check_points, _dot_mode, _grads_out, _hip_deslice_bwd,
     _hip_deslice_fwd, _hip_slice_bwd, _hip_slice_fwd, _param_grad_buffers, _point_dtype,
     _prep_wb, _small,
 )
@@ -73,13 +73,17 @@ def _hip_tied_bwd(x_mid, fx_mid, weight, bias, tau, tokens, d_out, dz_num, ds, d
         call = _Call(x_mid, weight, bias, tau, DV, dot)
         if _hip.lib().fs_family(call.prm) != 1:
             return None
+        _check_points(x_mid, fx_mid, DV, "fx_mid")
+        _check_points(x_mid, d_out, DV, "d_out")
         dt = _point_dtype(x_mid, fx_mid, d_out)
         x, fx, do = _as_points(x_mid, dt), _as_points(fx_mid, dt), _as_points(d_out, dt)
         dxm = torch.empty_like(x_mid, dtype=dt) if x_mid.stride(3) == 1 else \
             torch.empty(x_mid.shape, device=x.device, dtype=dt)
         dfx = torch.empty_like(fx_mid, dtype=dt) if fx_mid.stride(3) == 1 else \
             torch.empty(fx_mid.shape, device=x.device, dtype=dt)
-        tok, dz, dsv = _small(tokens), _small(dz_num), _small(ds)
+        tok = _small(tokens, (B, H, call.G, DV), "tokens")
+        dz = _small(dz_num, (B, H, call.G, DV), "dz_num")
+        dsv = _small(ds, (B, H, call.G), "ds")
         dtok = torch.empty(B, H, call.G, DV, device=x.device, dtype=torch.float32)
         dW, db, dtau = _param_grad_buffers(call)
         ws, nws = call.workspace(_hip.OP_TIED_BWD)

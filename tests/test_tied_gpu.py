@@ -106,3 +106,31 @@ def test_tied_matches_two_ops(shape):
             assert torch.equal(tied[k], two[k]), k
         else:
             assert e <= (2e-5 if k in ("db", "dtau") else 1e-5), (k, e)
+
+
+def test_operand_shapes_checked_before_launch():
+    """The library reads tokens, dz_num, ds, statistics and the second point
+    tensors through raw pointers: every op refuses a wrong shape with a
+    ValueError before anything is launched."""
+    ops = torch.ops.flashslice
+    B, N, H, D, G = 1, 300, 2, 32, 32
+    c = lambda *s: torch.randn(*s, device="cuda")  # noqa: E731
+    x, fx, W, b, tau = c(B, N, H, D), c(B, N, H, D), c(H, G, D), c(H, G), torch.ones(H).cuda()
+    tok, dz, ds = c(B, H, G, D), c(B, H, G, D), c(B, H, G)
+    with pytest.raises(ValueError, match="fx_mid has shape"):
+        ops.flash_slice(x, c(B, N - 1, H, D), W, b, tau, 0)
+    with pytest.raises(ValueError, match="tokens has shape"):
+        ops.flash_deslice(x, W, b, tau, c(B, H, G - 1, D), 0)
+    with pytest.raises(ValueError, match="dz_num has shape"):
+        ops.flash_slice_bwd(x, fx, W, b, tau, c(B, H, G, D - 1), ds, 0)
+    with pytest.raises(ValueError, match="ds has shape"):
+        ops.flash_slice_bwd(x, fx, W, b, tau, dz, c(B, H), 0)
+    with pytest.raises(ValueError, match="d_out has shape"):
+        ops.flash_deslice_bwd(x, W, b, tau, tok, c(B, N, H + 1, D), 0)
+    with pytest.raises(ValueError, match="stats has shape"):
+        ops.slice_blk(x, fx, W, b, tau, c(B, H, 2, N + 5), 0)
+    with pytest.raises(ValueError, match="d_out has shape"):
+        ops.deslice_slice_bwd(x, fx, W, b, tau, tok, c(B, 2 * N, H, D), dz, ds, 0)
+    with pytest.raises(ValueError, match="tokens has shape"):
+        ops.deslice_slice_bwd(x, fx, W, b, tau, c(2, H, G, D), x, dz, ds, 0)
+    torch.cuda.synchronize()
