@@ -900,10 +900,6 @@ __global__ __launch_bounds__(256, 1) void k_fused_tied_bwd(Args a) {
         for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xf[db]);
         FS_LOGITS(t2, xq)
       }
-      // each stage below is its own scheduling region: operand fragments are
-      // read from LDS next to their use rather than hoisted across stages
-      // (which runs the wider shapes out of registers)
-      sched_fence();
       // omega = fx . dz_num + d_out . tokens + ds, one accumulator per slot
       // block; one value block's split pieces live at a time
       {
@@ -940,7 +936,6 @@ __global__ __launch_bounds__(256, 1) void k_fused_tied_bwd(Args a) {
           for (int r = 0; r < 16; ++r) om[gb][r] = o[gb][r] + dsv[r];
         }
       }
-      sched_fence();
       {
         // d_out^T carrying the tile's sign (acc_add), split here when several
         // slot blocks share it, else next to its one use
@@ -954,7 +949,6 @@ __global__ __launch_bounds__(256, 1) void k_fused_tied_bwd(Args a) {
           if constexpr (NGB > 1) prep<MV>(oTq[vb], oT[vb]);
         }
         softmax_tile<NGB>(w, m2, lsum, t2, pv);
-        sched_fence();
         // dtokens += w^T d_out (rows of d_out beyond N read as zero), first:
         // d_out's transposed pieces die before dfx's accumulators are live
 #pragma unroll
@@ -969,7 +963,6 @@ __global__ __launch_bounds__(256, 1) void k_fused_tied_bwd(Args a) {
             mma_acc<MV>(dT[gb][vb], oTq[vb], wTq, sg);
           }
         }
-        sched_fence();
         // dfx = w dz_num (rows beyond N are not stored)
         {
           f32x16 o[NVB];
@@ -990,14 +983,12 @@ __global__ __launch_bounds__(256, 1) void k_fused_tied_bwd(Args a) {
 #pragma unroll
           for (int vb = 0; vb < NVB; ++vb) st_cols<T>(rdf, vcf[vb], (uint32_t)df_sn, o[vb]);
         }
-        sched_fence();
         dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
         // fx and d_out are reloaded for the wave's next tile only now: from
         // omega to here (the register peak) their buffers are dead, and dx,
         // dW and the next tile's logits still cover the loads' latency
         load_f(t + a.P);
         load_g(t + a.P);
-        sched_fence();
         FS_DX_DW(om, qWc, sg)
       }
     };
