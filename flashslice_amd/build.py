@@ -98,7 +98,29 @@ def build(verbose=False, jobs=None):
     os.replace(tmp, LIB_PATH)
     print("[build] wrote %s (%d units, %.0f s)" % (LIB_PATH, len(sources), time.time() - t0),
           flush=True)
+    _build_abi_smoke()
     return LIB_PATH
+
+
+ROOT = os.path.dirname(HERE)
+ABI_SMOKE_SRC = os.path.join(ROOT, "tests", "abi_smoke.cpp")
+ABI_SMOKE_BIN = os.path.join(ROOT, "tests", "_bin", "fs_abi_smoke")
+
+
+def _build_abi_smoke():
+    """The torch-free C ABI check (tests/abi_smoke.cpp): a host-only program
+    linked against the library, run by tests/test_abi_gpu.py."""
+    if not os.path.exists(ABI_SMOKE_SRC):
+        return
+    os.makedirs(os.path.dirname(ABI_SMOKE_BIN), exist_ok=True)
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    cmd = ["g++", "-O2", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(rocm, "include"),
+           ABI_SMOKE_SRC, "-o", ABI_SMOKE_BIN, "-L" + OUT_DIR, "-lflashslice_hip",
+           "-L" + os.path.join(rocm, "lib"), "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN/../../flashslice_amd/_lib"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("building the C ABI check failed:\n" + r.stderr[-4000:])
 
 
 def main(argv=None):

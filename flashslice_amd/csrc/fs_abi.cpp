@@ -292,15 +292,15 @@ Workspace plan_ws(int32_t op, const fs_slice_params* p, char* base) {
     return ptr;
   };
   const int64_t bh = p->B * p->H;
+  // the tied backward runs on the whole-G family only (else unsupported)
+  if (op == FS_OP_TIED_BWD && family_of(p) != 1) return w;
   // the fragment buffer: sized for the largest (fp32-accurate) fragments,
   // whatever the call's dtype
   const bool blocked = op == FS_OP_STATS || family_of(p) == 2;
   if (blocked && gp_on(p))
     w.frags = take((size_t)fs::gp_layout((int)p->B, (int)p->H, (int)p->G, (int)p->D, (int)p->DV,
                                          0).total_u32x4 * 4);
-  // the tied backward runs on the whole-G family only (else unsupported)
-  if (op == FS_OP_DESLICE_FWD || op == FS_OP_STATS ||
-      (op == FS_OP_TIED_BWD && family_of(p) != 1)) {
+  if (op == FS_OP_DESLICE_FWD || op == FS_OP_STATS) {
     w.bytes = off;
     return w;
   }

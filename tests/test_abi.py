@@ -150,3 +150,37 @@ def test_layernorm_validation_before_launch():
     assert rc == _hip.FS_ERR_INVALID and b"aligned" in lib.fs_last_error()
     rc = lib.fs_layernorm_bwd(p, p, p, p, p, p, p, p, p, 0, 100, 256, None)
     assert rc == _hip.FS_ERR_WORKSPACE
+
+
+def _pts(t, width):
+    return _hip.FsPoints(t.data_ptr(), 0, width, width, 0, width)
+
+
+def test_tied_and_row_splits_refused_before_launch():
+    """fs_tied_bwd serves the whole-G family only; row splits refuse the
+    G-blocked family and statistics. All of it is decided before a launch
+    (the host buffers passed here are never touched)."""
+    lib = _hip.lib()
+    buf = torch.zeros(64)
+    x = _pts(buf, 32)
+    p, keep = _params()
+    p.family = 2
+    rc = lib.fs_tied_bwd(ctypes.byref(x), ctypes.byref(x), ctypes.byref(x), ctypes.byref(p),
+                         *([ctypes.c_void_p(buf.data_ptr())] * 3), ctypes.byref(x), ctypes.byref(x),
+                         *([ctypes.c_void_p(buf.data_ptr())] * 4), None, 0, None)
+    assert rc == _hip.FS_ERR_UNSUPPORTED and b"whole-G kernels only" in lib.fs_last_error()
+    assert lib.fs_workspace_bytes(_hip.OP_TIED_BWD, ctypes.byref(p)) == 0
+    splits = torch.tensor([0, 60, 100], dtype=torch.int64)
+    p, keep = _params(B=2)
+    p.row_splits = splits.data_ptr()
+    rc = lib.fs_slice_fwd(ctypes.byref(x), ctypes.byref(x), ctypes.byref(p), None,
+                          ctypes.c_void_p(buf.data_ptr()), ctypes.c_void_p(buf.data_ptr()),
+                          ctypes.c_void_p(buf.data_ptr()), None, 0, None)
+    assert rc == _hip.FS_ERR_UNSUPPORTED and b"statistics" in lib.fs_last_error()
+    rc = lib.fs_compute_stats(ctypes.byref(x), ctypes.byref(p), ctypes.c_void_p(buf.data_ptr()),
+                              0, None, 0, None)
+    assert rc == _hip.FS_ERR_UNSUPPORTED and b"row splits" in lib.fs_last_error()
+    p.family = 2
+    rc = lib.fs_deslice_fwd(ctypes.byref(x), ctypes.byref(p), ctypes.c_void_p(buf.data_ptr()),
+                            None, None, ctypes.byref(x), None, 0, None)
+    assert rc == _hip.FS_ERR_UNSUPPORTED and b"whole-G" in lib.fs_last_error()
