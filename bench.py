@@ -1,7 +1,8 @@
 """Benchmark of the fused slice/deslice hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload c2|c3-256|c3-1024|c4|c5|ragged] [--tied]
+                    [--workload c2|c2-df|c3-256|c3-1024|c4|c5|c5-262k|ragged|layer|layer-1m-fwd]
+                    [--tied]
 
 One step is the coupling the metric names ("slice+deslice
 fwd+bwd ms & Mpoints/s at N=1M, H=8, D=32, G=32; peak HBM"): the four
@@ -72,6 +73,12 @@ MODEL_WORKLOADS = {
                n_layers=8, slice_num=32,
                desc="C5: Transolver fwd+bwd (MSE), B=1 N=2e6, n_hidden=256, 8 heads, 8 layers, "
                     "G=32, fp32, use_fused_slice=True"),
+    # the same model at the point count of the reference's published model
+    # number (README.md:137-142, N = 262k)
+    "c5-262k": dict(B=1, N=262_144, space_dim=3, fun_dim=1, out_dim=4, n_hidden=256, n_heads=8,
+                    n_layers=8, slice_num=32,
+                    desc="C5 model at N=262144: Transolver fwd+bwd (MSE), n_hidden=256, 8 heads, "
+                         "8 layers, G=32, fp32, use_fused_slice=True"),
 }
 # ragged batch (reference ROADMAP.md:66-68): many small meshes of different N
 # in one launch through row splits, against the per-sample loop it replaces
@@ -80,6 +87,17 @@ RAGGED_WORKLOADS = {
                    desc="ragged: 64 meshes of N ~ U[2000, 40000] (1.34M points), H=8 "
                         "D=DV=G=32 fp32 ieee, per-head W, slice->deslice fwd+bwd in one "
                         "launch per op through row splits"),
+}
+# one physics-attention layer, eager and fused in the same process (reference
+# bench/bench_layer.py: its default shape, training step)
+LAYER_WORKLOADS = {
+    "layer": dict(N=262_144, H=8, D=32, G=32, mode="train",
+                  desc="layer: Physics_Attention_Irregular_Mesh(256, heads=8, dim_head=32, "
+                       "slice_num=32), B=1 N=262144, fp32, training step (fwd + mean-square "
+                       "loss + bwd), fused vs eager"),
+    "layer-1m-fwd": dict(N=1_000_000, H=8, D=32, G=32, mode="fwd",
+                         desc="layer: Physics_Attention_Irregular_Mesh(256, heads=8, dim_head=32, "
+                              "slice_num=32), B=1 N=1e6, fp32, forward (no grad), fused vs eager"),
 }
 # dot level per run (reference slice_ops.py:336-343): 0 ieee; 3 bf16 (bf16 inputs)
 DOTS = {"ieee": 0, "bf16": 3}
@@ -328,6 +346,68 @@ def bench_ragged(a, cfg):
     print(json.dumps(line), flush=True)
 
 
+def bench_layer(a, cfg):
+    """The reference's layer-level number (bench/bench_layer.py:27-63): one
+    Physics_Attention_Irregular_Mesh training step, fused and eager in the
+    same process on the same weights and input, median of K event-timed
+    steps, and the peak memory one step allocates above what is resident."""
+    import statistics
+    from flashslice_amd.layers import Physics_Attention_Irregular_Mesh
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    N, H, D, G = cfg["N"], cfg["H"], cfg["D"], cfg["G"]
+    torch.manual_seed(0)
+    layer = Physics_Attention_Irregular_Mesh(H * D, heads=H, dim_head=D, slice_num=G,
+                                             use_fused_slice=True).to(dev)
+    assert layer.use_fused_slice
+    x = torch.randn(1, N, H * D, generator=torch.Generator().manual_seed(1)).to(dev)
+
+    def step():
+        if cfg["mode"] == "fwd":
+            with torch.no_grad():
+                layer(x)
+            return
+        out, _ = layer(x)
+        out.float().square().mean().backward()
+        layer.zero_grad(set_to_none=True)
+
+    res = {}
+    for fused in (True, False):
+        layer.use_fused_slice = fused
+        for _ in range(a.warmup):
+            step()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        base = torch.cuda.memory_allocated()
+        step()
+        torch.cuda.synchronize()
+        peak = (torch.cuda.max_memory_allocated() - base) / 1e9
+        ts = []
+        for _ in range(a.steps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            step()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        res[fused] = (statistics.median(ts), peak)
+        torch.cuda.empty_cache()
+    (fm, fp), (em, ep) = res[True], res[False]
+    line = {
+        "metric": "physics-attention layer %s Mpoints/s (fused)"
+                  % ("training step" if cfg["mode"] == "train" else "forward"),
+        "value": round(N / (fm * 1e-3) / 1e6, 3), "unit": "Mpoints/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(fm, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": cfg["desc"], "N": N, "H": H, "D": D, "G": G},
+        "eager_ms_per_step": round(em, 4), "speedup_vs_eager": round(em / fm, 3),
+        "peak_gb": {"fused": round(fp, 3), "eager": round(ep, 3)},
+        "roofline": None, "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def model_inputs(cfg, N, device, seed=0):
     """Coordinates uniform in the unit cube, per-point inputs and MSE targets
     ~N(0, 1), generated on the CPU from one seed."""
@@ -455,7 +535,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=None,
                     help="untimed steps first (default 5; 2 for the model workload)")
     ap.add_argument("--workload", default="c2",
-                    choices=sorted(WORKLOADS) + sorted(MODEL_WORKLOADS) + sorted(RAGGED_WORKLOADS))
+                    choices=sorted(WORKLOADS) + sorted(MODEL_WORKLOADS) + sorted(RAGGED_WORKLOADS)
+                    + sorted(LAYER_WORKLOADS))
     ap.add_argument("--dot", default="ieee", choices=sorted(DOTS),
                     help="dot level: ieee (fp32 inputs) or bf16 (x_mid, fx_mid, W in bf16)")
     ap.add_argument("--tied", action="store_true",
@@ -482,6 +563,8 @@ def main():
 
     if a.workload in MODEL_WORKLOADS:
         return bench_model(a, MODEL_WORKLOADS[a.workload])
+    if a.workload in LAYER_WORKLOADS:
+        return bench_layer(a, LAYER_WORKLOADS[a.workload])
     if a.workload in RAGGED_WORKLOADS:
         torch.cuda.set_device(0)
         return bench_ragged(a, RAGGED_WORKLOADS[a.workload])

@@ -10,3 +10,17 @@ into ``flashslice_amd/_lib/libflashslice_hip.so`` by
 """
 
 __version__ = "0.1.0"
+
+# The reference package root exports its model and layer classes
+# (reference flashslice/__init__.py:18-27); loaded on first use, so that
+# ``python -m flashslice_amd.build`` does not import torch.
+_LAYER_NAMES = ("Transolver", "TransolverBlock", "TokenTransformerBlock",
+                "Physics_Attention_Irregular_Mesh")
+__all__ = list(_LAYER_NAMES) + ["__version__"]
+
+
+def __getattr__(name):
+    if name in _LAYER_NAMES:
+        from . import layers
+        return getattr(layers, name)
+    raise AttributeError("module 'flashslice_amd' has no attribute %r" % name)

@@ -167,3 +167,14 @@ def test_layernorm_op_compiles_to_one_graph():
     assert explain.graph_break_count == 0, explain.break_reasons
     y, mean, rstd = torch.ops.flashslice_layer.layer_norm(x, w, w, 1e-5)
     assert y.shape == x.shape and mean.shape == (70000,) and rstd.dtype == torch.float32
+
+
+def test_package_root_exports_the_models():
+    """``from flashslice_amd import Transolver`` as the reference's
+    ``from flashslice import Transolver`` (reference flashslice/__init__.py:18-27)."""
+    import flashslice_amd
+    from flashslice_amd import layers
+    for name in ("Transolver", "TransolverBlock", "TokenTransformerBlock",
+                 "Physics_Attention_Irregular_Mesh"):
+        assert getattr(flashslice_amd, name) is getattr(layers, name)
+    assert flashslice_amd.__version__
