@@ -120,7 +120,12 @@ def _build_abi_smoke():
            "-Wl,-rpath,$ORIGIN/../../flashslice_amd/_lib"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError("building the C ABI check failed:\n" + r.stderr[-4000:])
+        # a test helper: the library itself is built; tests/test_abi_gpu.py
+        # reports the missing program
+        print("[build] WARNING: the C ABI check (tests/abi_smoke.cpp) did not build:\n"
+              + r.stderr[-2000:], flush=True)
+        return
+    print("[build] wrote %s" % ABI_SMOKE_BIN, flush=True)
 
 
 def main(argv=None):

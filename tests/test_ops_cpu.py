@@ -235,3 +235,19 @@ def test_varlen_fakes_autograd_and_validation():
     with pytest.raises(NotImplementedError):  # no CPU fallback
         fused_slice_varlen(torch.randn(10, 2, 4), torch.randn(10, 2, 4), torch.randn(3, 4),
                            None, torch.ones(2), [0, 4, 10])
+
+
+def test_varlen_compile_keeps_one_graph():
+    import torch._dynamo
+    from flashslice_amd.kernels import fused_deslice_varlen, fused_slice_varlen
+
+    def coupling(x, fx, w, b, tau, rs):
+        z, s = fused_slice_varlen(x, fx, w, b, tau, rs, max_rows=60)
+        return fused_deslice_varlen(x, w, b, tau, z / (s + 1e-5)[..., None], rs, max_rows=60)
+
+    torch._dynamo.reset()
+    m = lambda *s, **k: torch.empty(*s, device="meta", **k)  # noqa: E731
+    explain = torch._dynamo.explain(coupling)(m(100, 3, 8), m(100, 3, 8), m(3, 5, 8), m(3, 5),
+                                              m(3), m(4, dtype=torch.int64))
+    assert explain.graph_break_count == 0, explain.break_reasons
+    assert explain.graph_count == 1
