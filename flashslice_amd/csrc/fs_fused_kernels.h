@@ -251,7 +251,76 @@ __global__ __launch_bounds__(256, NGB * NDB * NVB == 1 ? 3 : 1) void k_fused_sli
     };
     FS_TILE_LOOP(load, body, true, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
   };
-  if (fast) run(std::true_type()); else run(std::false_type());
+  // The wider shapes: one buffer per point stream, each reloaded for the
+  // wave's next tile right after its last use (x after the logits, fx once
+  // split, after the softmax): 349 registers instead of 393 at C4's shape,
+  // still one wave per SIMD, 4 % faster there (1.009 against 1.053 ms; fitted
+  // to 256 registers for two waves it spills and takes 1.93 ms).
+  auto run_wide = [&](auto fast_c) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
+    float xb[NDB][16], fb[NVB][16];
+    auto load_x = [&](int t) {
+      ld_rows<T, NDB, FAST>(xb, rows_rsrc(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
+    };
+    auto load_f = [&](int t) {
+      const Rsrc rf = rows_rsrc(f_b, f_sn, f_w, (int64_t)t * kTile, N);
+#pragma unroll
+      for (int vb = 0; vb < NVB; ++vb) ld_cols<T>(fb[vb], rf, vcf[vb], (uint32_t)f_sn);
+    };
+    auto body = [&](int t, auto par) {
+      const int64_t p0 = (int64_t)t * kTile;
+      const bool pv = p0 + c < N;
+      constexpr float sg = decltype(par)::sign;
+      float t2[NGB][16], w[NGB][16], m2, lsum;
+      {
+        Frag<ML> xq[NDB];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) prep<ML>(xq[db], xb[db]);
+        FS_LOGITS(t2, xq)
+      }
+      load_x(t + a.P);
+      softmax_tile<NGB>(w, m2, lsum, t2, pv);
+      store_stats_tile(st_m, st_l, p0, N, c, h, m2, lsum);
+      Frag<MV> fq[NVB];  // fx carries the tile's sign (acc_add)
+#pragma unroll
+      for (int vb = 0; vb < NVB; ++vb) {
+        float fs[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) fs[j] = fb[vb][j] * sg;
+        prep<MV>(fq[vb], fs);
+      }
+      load_f(t + a.P);
+#pragma unroll
+      for (int gb = 0; gb < NGB; ++gb) {
+        float wT[16];
+        transpose32(wT, w[gb], lds, c, h);
+        Frag<MV> wq;
+        prep<MV>(wq, wT);
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) mma_acc<MV>(zacc[gb][vb], fq[vb], wq, sg);
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s += wT[j];
+        sacc[gb] += s;
+      }
+    };
+    int t = pid;
+    load_x(t);
+    load_f(t);
+    while (t < ntiles_) {
+      body(t, TileEven());
+      t += a.P;
+      if (t >= ntiles_) break;
+      body(t, TileOdd());
+      t += a.P;
+    }
+  };
+  if constexpr (NGB * NDB * NVB > 1) {
+    if (fast) run_wide(std::true_type()); else run_wide(std::false_type());
+  } else {
+    if (fast) run(std::true_type()); else run(std::false_type());
+  }
   float ssum[NGB];
 #pragma unroll
   for (int gb = 0; gb < NGB; ++gb) ssum[gb] = pair_sum(sacc[gb]);
