@@ -103,13 +103,16 @@ def test_varlen_parity(name, lens, H, D, DV, G, layout):
     assert not fails, "\n".join(fails)
 
 
-def test_varlen_matches_per_sample_ops():
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_varlen_matches_per_sample_ops(dtype):
     """One ragged launch against each sample through the regular operators
     (B = 1 calls): the same values up to summation order (1e-5 relative),
-    since the partition of a sample's tiles depends on the launch."""
+    since the partition of a sample's tiles depends on the launch; bf16
+    point tensors (fp32-accurate dots, fp32 sums) likewise."""
     lens, H, D, G = [4097, 100, 2500], 8, 32, 32
     L, _, _ = _inputs(lens, H, D, D, G, "hgd")
     dev = {k: v.cuda() for k, v in L.items()}
+    dev["x"], dev["fx"] = dev["x"].to(dtype), dev["fx"].to(dtype)
     splits = [0, 4097, 4197, 6697]
     tok = torch.randn(3, H, G, D).cuda()
     z, s = fused_slice_varlen(dev["x"], dev["fx"], dev["w"], dev["b"], dev["tau"], splits)
