@@ -126,3 +126,42 @@ def test_varlen_matches_per_sample_ops(dtype):
         assert relerr(z[i], z1[0]) < 1e-5 and relerr(s[i], s1[0]) < 1e-5, i
         # a row's deslice involves no cross-tile sum: bitwise equal
         assert torch.equal(out[sl], o1[0]), i
+
+
+def test_varlen_bench_shape():
+    """The ragged bench's shape (64 meshes of N ~ U[2000, 40000], H = 8,
+    D = DV = G = 32): one launch per op against per-mesh calls of the
+    regular operators -- slot sums within 1e-5, deslice rows bitwise, and
+    the slice backward's dx / dfx within 1e-5 -- and two launches bitwise
+    equal."""
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(2000, 40001, (64,), generator=g).tolist()
+    splits = [0]
+    for n in lens:
+        splits.append(splits[-1] + n)
+    rows, H, D, G = splits[-1], 8, 32, 32
+    x = torch.randn(rows, H, D, generator=g).cuda()
+    fx = torch.randn(rows, H, D, generator=g).cuda()
+    W = (torch.randn(H, G, D, generator=g) / math.sqrt(D)).cuda()
+    b = (0.02 * torch.randn(H, G, generator=g)).cuda()
+    tau = (0.3 + 0.7 * torch.rand(H, generator=g)).cuda()
+    tok = torch.randn(64, H, G, D, generator=g).cuda()
+    dz = torch.randn(64, H, G, D, generator=g).cuda()
+    ds = torch.randn(64, H, G, generator=g).cuda()
+    rs = torch.tensor(splits, dtype=torch.int64).cuda()
+    ops = torch.ops.flashslice
+    nmax = max(lens)
+    z, s = ops.slice_varlen(x, fx, W, b, tau, rs, nmax, 0)
+    out = ops.deslice_varlen(x, W, b, tau, tok, rs, nmax, 0)
+    dx, dfx, _, _, _ = ops.slice_varlen_bwd(x, fx, W, b, tau, rs, nmax, dz, ds, 0)
+    z2, s2 = ops.slice_varlen(x, fx, W, b, tau, rs, nmax, 0)
+    assert torch.equal(z, z2) and torch.equal(s, s2)
+    for i in range(0, 64, 7):
+        sl = slice(splits[i], splits[i + 1])
+        xi, fi = x[sl][None], fx[sl][None]
+        z1, s1 = ops.flash_slice(xi, fi, W, b, tau, 0)
+        o1 = ops.flash_deslice(xi, W, b, tau, tok[i:i + 1], 0)
+        dx1, dfx1, _, _, _ = ops.flash_slice_bwd(xi, fi, W, b, tau, dz[i:i + 1], ds[i:i + 1], 0)
+        assert relerr(z[i], z1[0]) < 1e-5 and relerr(s[i], s1[0]) < 1e-5, i
+        assert torch.equal(out[sl], o1[0]), i
+        assert relerr(dx[sl], dx1[0]) < 1e-5 and relerr(dfx[sl], dfx1[0]) < 1e-5, i
