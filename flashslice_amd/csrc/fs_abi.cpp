@@ -107,9 +107,12 @@ int64_t fused_target(int32_t op, const fs_slice_params* p) {
   int64_t t;
   switch (op) {
     case FS_OP_DESLICE_BWD: t = 512; break;
-    // one wave per SIMD, one 125 KB block per CU at C4: one dispatch round
-    // (measured at C4 against 512 / 1024 / 2048 blocks: 1 / 3 / 9 % faster)
-    case FS_OP_TIED_BWD: t = 256; break;
+    // wider shapes: one wave per SIMD, one 125 KB block per CU at C4, one
+    // dispatch round (measured at C4 against 512 / 1024 / 2048 blocks: 1 / 3 /
+    // 9 % faster); one block of 32 on every axis: two waves per SIMD, 1024
+    // blocks (C2's shape: 1.193 / 1.137 / 1.146 / 1.151 ms at 512 / 1024 /
+    // 1536 / 2048)
+    case FS_OP_TIED_BWD: t = one ? 1024 : 256; break;
     case FS_OP_SLICE_FWD: t = one ? 1536 : 512; break;
     case FS_OP_DESLICE_FWD: t = one ? 2048 : 1536; break;
     default: t = 1536;

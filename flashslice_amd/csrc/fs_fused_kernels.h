@@ -890,9 +890,11 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
 // two backward kernels' 4 + 3 and autograd's sum of their two dx (3 more).
 // Value fragments in LDS: dz_num [g, v] (omega) and [v, g] (dfx), tokens
 // [g, v] (omega), W / tau [d, g] (dx). Partials in the deslice-bwd layout.
-// One wave per SIMD for every shape (the slot accumulators of both ops).
+// Two waves per SIMD for one block of 32 on every axis (256 registers; the
+// aligned-row tile path does not spill: 1.283 -> 1.137 ms at C2's shape with
+// 1024 blocks), one for the wider shapes (the slot accumulators of both ops).
 template <typename T, int DK, int NGB, int NDB, int NVB>
-__global__ __launch_bounds__(256, 1) void k_fused_tied_bwd(Args a) {
+__global__ __launch_bounds__(256, (NGB * NDB * NVB == 1) ? 2 : 1) void k_fused_tied_bwd(Args a) {
   FS_PROLOGUE(NGB, NDB, NVB, 3 * NGB * NVB + NDB * NGB, kLdsTile)
   static_assert(SM::TOTAL * 4 <= 160 * 1024, "tied backward LDS exceeds 160 KB");
   u32x4* qZr = qV;
