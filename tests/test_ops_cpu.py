@@ -251,3 +251,15 @@ def test_varlen_compile_keeps_one_graph():
                                               m(3), m(4, dtype=torch.int64))
     assert explain.graph_break_count == 0, explain.break_reasons
     assert explain.graph_count == 1
+
+
+def test_varlen_device_splits_need_max_rows():
+    from flashslice_amd.kernels import fused_slice_varlen
+    m = lambda *s, **k: torch.empty(*s, device="meta", **k)  # noqa: E731
+    x, w, b, tau = m(100, 3, 8), m(3, 5, 8), m(3, 5), m(3)
+    with pytest.raises(ValueError, match="need max_rows"):
+        fused_slice_varlen(x, x, w, b, tau, m(4, dtype=torch.int64))
+    with pytest.raises(ValueError, match="1-d int64"):
+        fused_slice_varlen(x, x, w, b, tau, m(4, dtype=torch.int32), max_rows=50)
+    z, s = fused_slice_varlen(x, x, w, b, tau, m(4, dtype=torch.int64), max_rows=50)
+    assert z.shape == (3, 3, 5, 8) and s.shape == (3, 3, 5)

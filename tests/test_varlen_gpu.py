@@ -156,6 +156,11 @@ def test_varlen_bench_shape():
     dx, dfx, _, _, _ = ops.slice_varlen_bwd(x, fx, W, b, tau, rs, nmax, dz, ds, 0)
     z2, s2 = ops.slice_varlen(x, fx, W, b, tau, rs, nmax, 0)
     assert torch.equal(z, z2) and torch.equal(s, s2)
+    # the public API with device row splits (trusted, max_rows given) and
+    # with host row splits (validated, copied) launch the same kernels
+    z3, s3 = fused_slice_varlen(x, fx, W, b, tau, rs, max_rows=nmax)
+    z4, s4 = fused_slice_varlen(x, fx, W, b, tau, splits)
+    assert torch.equal(z, z3) and torch.equal(s, s3) and torch.equal(z, z4) and torch.equal(s, s4)
     for i in range(0, 64, 7):
         sl = slice(splits[i], splits[i + 1])
         xi, fi = x[sl][None], fx[sl][None]
