@@ -91,11 +91,11 @@ Geo geo_g(const fs_slice_params* p, int dk) {
 }
 
 // Blocks per launch of the whole-G kernels (measured on MI355X at C2: N = 1e6,
-// H = 8, D = DV = G = 32, and at C4: G = 64, DV = 64): the kernels run best
-// with several times more blocks than stay resident, so that the hardware
-// keeps refilling CUs as blocks finish -- except the deslice backward, whose
-// blocks each stream long runs of tiles, and the slice forward of the wider
-// shapes (one wave per SIMD; C4 5 % slower at 1024 blocks than at 512).
+// H = 8, D = DV = G = 32, and at C4: G = 64, DV = 64): at C2's shape the
+// kernels run best with several times more blocks than stay resident, so
+// that the hardware keeps refilling CUs as blocks finish -- except the
+// deslice backward, whose blocks each stream long runs of tiles; the wider
+// shapes' one-wave-per-SIMD kernels run best in one dispatch round.
 // A ragged batch (row splits) sizes its grid by the longest sample, so every
 // (sample, head) gets the same blocks: at least 8 each, so that the longest
 // samples' tiles are spread over enough waves to keep the tail short
@@ -113,12 +113,16 @@ int64_t fused_target(int32_t op, const fs_slice_params* p) {
     // blocks (C2's shape: 1.193 / 1.137 / 1.146 / 1.151 ms at 512 / 1024 /
     // 1536 / 2048)
     case FS_OP_TIED_BWD: t = one ? 1024 : 256; break;
-    case FS_OP_SLICE_FWD: t = one ? 1536 : 512; break;
+    // wider shapes: one wave per SIMD, one dispatch round (C4: 0.973 ms
+    // against 0.995 at 512 blocks)
+    case FS_OP_SLICE_FWD: t = one ? 1536 : 256; break;
     // wider shapes: one wave per SIMD and one 100 KB block per CU at C4, one
     // dispatch round (measured at C4: 1.99 ms against 2.13 at 1536 blocks,
     // 2.03 at 512)
     case FS_OP_SLICE_BWD: t = one ? 1536 : 256; break;
-    case FS_OP_DESLICE_FWD: t = one ? 2048 : 1536; break;
+    // wider shapes: two waves per SIMD (C4: 0.680 ms at 1024 blocks against
+    // 0.690 / 0.684 / 0.696 at 1536 / 512 / 2048)
+    case FS_OP_DESLICE_FWD: t = one ? 2048 : 1024; break;
     default: t = 1536;
   }
   const int64_t rt = kRaggedBlocksPerBH * p->B * p->H;
