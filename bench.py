@@ -1,7 +1,7 @@
 """Benchmark of the fused slice/deslice hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload c2|c2-df|c3-256|c3-1024|c4|c5|c5-262k|ragged|layer|layer-1m-fwd]
+                    [--workload c1|c2|c2-df|c3-256|c3-1024|c4|c5|c5-262k|ragged|layer|layer-1m-fwd]
                     [--tied]
 
 One step is the coupling the metric names ("slice+deslice
@@ -346,6 +346,75 @@ def bench_ragged(a, cfg):
     print(json.dumps(line), flush=True)
 
 
+def bench_c1(a):
+    """BASELINE config 1, the reference's CPU-runnable case: slice then
+    deslice, forward only, B=1, N=4096, H=8, D=DV=G=32, shared W ~ N(0, 1/D),
+    no bias, tau = 0.5, tokens = z_num / (s + 1e-5); seed 0. Reports the
+    step's time (launch-bound at this size), its error against the CPU
+    oracle in float64 and the oracle's own fp32 time on this host."""
+    import oracle
+    from flashslice_amd.kernels import fused_deslice, fused_slice
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, N, H, D, G = 1, 4096, 8, 32, 32
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(B, N, H, D, generator=g)
+    fx = torch.randn(B, N, H, D, generator=g)
+    W = torch.randn(G, D, generator=g) / D ** 0.5
+    tau = torch.full((H,), 0.5)
+    xd, fd, Wd, td = (t.to(dev) for t in (x, fx, W, tau))
+
+    def step():
+        z, s_ = fused_slice(xd, fd, Wd, None, td)
+        return fused_deslice(xd, Wd, None, td, z / (s_ + 1e-5)[..., None]), z, s_
+
+    for _ in range(a.warmup):
+        step()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(a.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e0, e1 in ev:
+        e0.record()
+        res = step()
+        e1.record()
+    torch.cuda.synchronize()
+    ms = 1e3 * (time.perf_counter() - t0) / a.steps
+    ms_med = sorted(e0.elapsed_time(e1) for e0, e1 in ev)[a.steps // 2]
+    ref = oracle.coupling(x.double(), fx.double(), W.double(), None, tau.double(),
+                          order="slice-first")
+    err = {k: float((r.detach().double().cpu() - t.double()).norm() / t.norm())
+           for k, r, t in zip(("out", "z_num", "s"), res, ref)}
+    torch.set_num_threads(os.cpu_count() or 1)
+    ts = []
+    for _ in range(4):
+        t1 = time.perf_counter()
+        oracle.coupling(x, fx, W, None, tau, order="slice-first")
+        ts.append(time.perf_counter() - t1)
+    cpu_s = sorted(ts[1:])[1]
+    nbytes = B * N * H * 4 * D * 4
+    line = {
+        "metric": "slice+deslice forward Mpoints/s (config 1)",
+        "value": round(B * N / (ms_med * 1e-3) / 1e6, 3), "unit": "Mpoints/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 4),
+        "ms_per_step_median": round(ms_med, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "C1: slice->deslice forward only, B=1 N=4096 H=8 D=DV=G=32, "
+                               "shared W, no bias, tau=0.5", "B": B, "N": N, "H": H, "D": D,
+                   "G": G},
+        "roofline": {"bound": "launch latency", "achieved": round(nbytes / (ms_med * 1e-3) / 1e9, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(nbytes / (ms_med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "alg_bytes_per_step": nbytes},
+        "relerr_vs_float64_oracle": {k: float("%.3g" % v) for k, v in err.items()},
+        "cpu_baseline": {"value": round(B * N / cpu_s / 1e6, 4), "unit": "Mpoints/s",
+                         "cores": torch.get_num_threads(), "kind": "port",
+                         "sample": "eager PyTorch softmax/einsum oracle (oracle/eager.py), fp32 "
+                                   "forward of the whole config, median of 3 runs after 1"},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def bench_layer(a, cfg):
     """The reference's layer-level number (bench/bench_layer.py:27-63): one
     Physics_Attention_Irregular_Mesh training step, fused and eager in the
@@ -536,7 +605,7 @@ def main():
                     help="untimed steps first (default 5; 2 for the model workload)")
     ap.add_argument("--workload", default="c2",
                     choices=sorted(WORKLOADS) + sorted(MODEL_WORKLOADS) + sorted(RAGGED_WORKLOADS)
-                    + sorted(LAYER_WORKLOADS))
+                    + sorted(LAYER_WORKLOADS) + ["c1"])
     ap.add_argument("--dot", default="ieee", choices=sorted(DOTS),
                     help="dot level: ieee (fp32 inputs) or bf16 (x_mid, fx_mid, W in bf16)")
     ap.add_argument("--tied", action="store_true",
@@ -563,6 +632,8 @@ def main():
 
     if a.workload in MODEL_WORKLOADS:
         return bench_model(a, MODEL_WORKLOADS[a.workload])
+    if a.workload == "c1":
+        return bench_c1(a)
     if a.workload in LAYER_WORKLOADS:
         return bench_layer(a, LAYER_WORKLOADS[a.workload])
     if a.workload in RAGGED_WORKLOADS:
