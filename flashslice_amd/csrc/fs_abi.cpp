@@ -152,6 +152,9 @@ int32_t check_params(const fs_slice_params* p, const char* who) {
     return fail(FS_ERR_INVALID, "%s: dot level %d is not in [0, 4]", who, p->dot);
   if (p->family < 0 || p->family > 2)
     return fail(FS_ERR_INVALID, "%s: family %d is not 0, 1 or 2", who, p->family);
+  if (p->row_splits && (p->total_rows < 1 || p->total_rows > (int64_t)0x7fffffff - 64))
+    return fail(FS_ERR_INVALID, "%s: total_rows = %lld must be in [1, 2^31 - 64] with row splits",
+                who, (long long)p->total_rows);
   return FS_OK;
 }
 
@@ -230,6 +233,7 @@ fs::Args base_args(const fs_slice_params* p, const Geo& g) {
   a.nd = (int)((p->D + 31) / 32);
   a.nv = (int)((p->DV + 31) / 32);
   a.rows = p->row_splits;
+  a.rows_total = p->row_splits ? p->total_rows : 0;
   return a;
 }
 

@@ -92,6 +92,10 @@ __device__ __forceinline__ void block_partial(float* buf, int E, int wid, float*
   __syncthreads();
 }
 __device__ __forceinline__ void acc_put(float& t, float v, bool first) { t = first ? v : t + v; }
+// a row split held to [lo, hi] (ragged batches: splits are read on the device only)
+__device__ __forceinline__ int64_t clamp_rows(int64_t v, int64_t lo, int64_t hi) {
+  return v < lo ? lo : (v > hi ? hi : v);
+}
 
 // Block prologue shared by the four kernels: head constants, LDS carve-up,
 // the fp32 staging of W and tokens / dz_num, and the logits operand W
@@ -108,10 +112,12 @@ __device__ __forceinline__ void acc_put(float& t, float v, bool first) { t = fir
   const int bh = blockIdx.y;                                                        \
   const int b = bh / a.H, hd = bh - b * a.H;                                       \
   const int pid = blockIdx.x * kWavesPerBlock + wid;                                \
-  /* row splits (ragged batch): sample b is rows rows[b] .. rows[b + 1] - 1 */      \
-  const int64_t row0_ = a.rows ? a.rows[b] : 0;                                     \
+  /* row splits (ragged batch): sample b is rows rows[b] .. rows[b + 1] - 1,      \
+     clamped to the point tensors' rows and to N rows per sample */                 \
+  const int64_t row0_ = a.rows ? clamp_rows(a.rows[b], 0, a.rows_total) : 0;        \
   const int G = a.G, D = a.D, DV = a.DV;                                            \
-  const int N = a.rows ? (int)(a.rows[b + 1] - row0_) : a.N;                        \
+  const int N = a.rows ? (int)min(clamp_rows(a.rows[b + 1], row0_, a.rows_total) - row0_, \
+                                  (int64_t)a.N) : a.N;                              \
   const int ntiles_ = a.rows ? (N + kTile - 1) / kTile : a.ntiles;                  \
   float* sW = smem;                                                                 \
   float* sV = smem + SM::GP * SM::SW;                                               \

@@ -33,6 +33,7 @@ struct Args {
   float* part2;                            // per-wave dtau partials of point-owned kernels
   const int64_t* rows;                     // row splits (B + 1) of a ragged batch, or null
                                            // (whole-G family; point strides along b are 0)
+  int64_t rows_total;                      // rows of the ragged batch's point tensors
   int B, N, H, D, DV, G;
   int P;                                   // point partitions per (b, h), a multiple of 4
   int ntiles;                              // ceil(N / 32)

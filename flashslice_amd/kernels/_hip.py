@@ -44,7 +44,7 @@ class FsSliceParams(ctypes.Structure):
                 ("b_stride_b", ctypes.c_int64), ("b_stride_h", ctypes.c_int64),
                 ("tau", ctypes.c_void_p),
                 ("dot", ctypes.c_int32), ("family", ctypes.c_int32),
-                ("row_splits", ctypes.c_void_p)]
+                ("row_splits", ctypes.c_void_p), ("total_rows", ctypes.c_int64)]
 
 
 class FlashSliceLibError(RuntimeError):

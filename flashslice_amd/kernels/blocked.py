@@ -31,9 +31,9 @@ _BLOCK_G = None  # None = automatic; set_block_g overrides
 
 def set_block_g(gb):
     """Force the G-block size (a power of two >= 16), or None for automatic
-    (reference ``blocked.py:87-94``). The HIP kernels work in blocks of 32
-    slots; a forced size sets how many of them one wave holds (gb / 32,
-    at least one)."""
+    (reference ``blocked.py:87-94``). The value is validated as the
+    reference's and reported by ``tiles()``; the HIP kernels always work in
+    slot blocks of 32 (one MFMA tile), so it does not change them."""
     global _BLOCK_G
     if gb is not None and (gb < 16 or (gb & (gb - 1)) != 0):
         raise ValueError("block size must be a power of two >= 16, got %r" % gb)

@@ -209,7 +209,7 @@ def _prep_wb(x_mid, weight, bias):
         raise ValueError("weight's last dim is %d, x_mid's head width is %d"
                          % (weight.shape[-1], D))
     if bias is None:
-        bias = weight.new_zeros(G)
+        bias = _zero_bias(weight, G)
     elif bias.dim() not in (1, 2, 3) or bias.shape[-1] != G:
         raise ValueError("bias must be (G,), (H, G) or (B, H, G) with G=%d, "
                          "got shape %s" % (G, tuple(bias.shape)))
@@ -249,13 +249,48 @@ def _as_points(t, dtype):
     return t
 
 
+def _same_device(x_mid, **tensors):
+    """Every tensor operand of a call on x_mid's device. The library takes
+    raw device pointers: a host tensor handed to a kernel would be read (or
+    written) from the GPU and fault it, so it is refused before any launch
+    (the reference's Triton launch raises on it too)."""
+    dev = x_mid.device
+    for name, t in tensors.items():
+        if t is not None and t.device != dev:
+            raise ValueError("%s is on %s, x_mid on %s: every tensor of a fused call must be "
+                             "on x_mid's device" % (name, t.device, dev))
+
+
+_ZERO_BIAS = {}
+
+
+def _zero_bias(weight, G):
+    """zeros(G) in weight's dtype and device for a None bias, cached per
+    (device, dtype, G) outside compiled regions (an allocation less per op
+    call); the tensor is only read by the kernels."""
+    if torch.compiler.is_compiling():
+        return weight.new_zeros(G)
+    key = (weight.device, weight.dtype, G)
+    z = _ZERO_BIAS.get(key)
+    if z is None:
+        z = _ZERO_BIAS[key] = weight.new_zeros(G)
+    return z
+
+
+_WS_BYTES = {}
+
+
 class _Call:
     """The fp32 small operands and the FsSliceParams of one call (holding
     references so the converted tensors outlive the launch)."""
 
     def __init__(self, x_mid, weight, bias, tau, dv, dot, rows=None):
         B, N, H, D = x_mid.shape
+        _same_device(x_mid, weight=weight, bias=bias, tau=tau,
+                     row_splits=None if rows is None else rows[0])
+        total_rows = 0
         if rows is not None:
+            total_rows = N
             # ragged batch (varlen.py): x_mid is the (1, rows, H, D) view of the
             # concatenated samples; rows = (row splits on the device, samples,
             # longest sample)
@@ -275,12 +310,21 @@ class _Call:
                                       self.weight.data_ptr(), swb, swh,
                                       self.bias.data_ptr(), sbb, sbh,
                                       self.tau.data_ptr(), int(dot), family,
-                                      None if rows is None else rows[0].data_ptr())
+                                      None if rows is None else rows[0].data_ptr(),
+                                      total_rows)
         self.rows = rows  # keeps the row splits alive across the launch
         self.B, self.N, self.H, self.D, self.DV, self.G = B, N, H, D, dv, G
+        self._key = (B, N, H, D, dv, G, swb, swh, sbb, sbh, int(dot), family, rows is not None,
+                     total_rows)
 
     def workspace(self, op):
-        n = _hip.lib().fs_workspace_bytes(op, self.prm)
+        """A workspace of fs_workspace_bytes for this op; the size is a
+        function of the shape, layout, dot level and family only, so it is
+        asked for once per such key."""
+        key = (op,) + self._key
+        n = _WS_BYTES.get(key)
+        if n is None:
+            n = _WS_BYTES[key] = _hip.lib().fs_workspace_bytes(op, self.prm)
         if n == 0:
             return None, 0
         return torch.empty(n, dtype=torch.uint8, device=self.device), n
@@ -289,17 +333,23 @@ class _Call:
         return _hip.stream_of(self.device)
 
 
-def _small(t, shape, name):
+def _small(t, shape, name, device):
     """A small per-slot tensor (tokens, dz_num, ds, stats) as fp32
-    contiguous, after checking its shape: the library reads it through a raw
-    pointer, so a wrong size must be refused before the launch."""
+    contiguous, after checking its shape and device: the library reads it
+    through a raw pointer, so a wrong size or a host tensor must be refused
+    before the launch."""
+    if t.device != device:
+        raise ValueError("%s is on %s, x_mid on %s: every tensor of a fused call must be "
+                         "on x_mid's device" % (name, t.device, device))
     if tuple(t.shape) != tuple(shape):
         raise ValueError("%s has shape %s, expected %s" % (name, tuple(t.shape), tuple(shape)))
     return t.detach().to(torch.float32).contiguous()
 
 
 def _check_points(x_mid, t, width, name):
-    """A second point tensor of a call: x_mid's (B, N, H) and ``width``."""
+    """A second point tensor of a call: x_mid's (B, N, H), ``width`` and
+    device."""
+    _same_device(x_mid, **{name: t})
     if t.dim() != 4 or tuple(t.shape[:3]) != tuple(x_mid.shape[:3]) or t.shape[3] != width:
         raise ValueError("%s has shape %s, expected %s" % (
             name, tuple(t.shape), tuple(x_mid.shape[:3]) + (width,)))
@@ -317,7 +367,7 @@ def _hip_slice_fwd(x_mid, fx_mid, weight, bias, tau, dot, stats_in=None, want_st
         x, fx = _as_points(x_mid, dt), _as_points(fx_mid, dt)
         z_num = torch.empty(B, H, call.G, DV, device=x.device, dtype=torch.float32)
         s = torch.empty(B, H, call.G, device=x.device, dtype=torch.float32)
-        st_in = None if stats_in is None else _small(stats_in, (B, H, 2, N), "stats")
+        st_in = None if stats_in is None else _small(stats_in, (B, H, 2, N), "stats", x.device)
         st_out = (torch.empty(B, H, 2, N, device=x.device, dtype=torch.float32)
                   if want_stats and st_in is None else None)
         ws, nws = call.workspace(_hip.OP_SLICE_FWD)
@@ -335,9 +385,9 @@ def _hip_deslice_fwd(x_mid, weight, bias, tau, tokens, dot, stats_in=None, want_
         call = _Call(x_mid, weight, bias, tau, DV, dot, rows)
         dt = _point_dtype(x_mid)
         x = _as_points(x_mid, dt)
-        tok = _small(tokens, (call.B, H, call.G, DV), "tokens")
+        tok = _small(tokens, (call.B, H, call.G, DV), "tokens", x.device)
         out = torch.empty(B, N, H, DV, device=x.device, dtype=dt)
-        st_in = None if stats_in is None else _small(stats_in, (B, H, 2, N), "stats")
+        st_in = None if stats_in is None else _small(stats_in, (B, H, 2, N), "stats", x.device)
         st_out = (torch.empty(B, H, 2, N, device=x.device, dtype=torch.float32)
                   if want_stats and st_in is None else None)
         ws, nws = call.workspace(_hip.OP_DESLICE_FWD)
@@ -380,9 +430,9 @@ def _hip_slice_bwd(x_mid, fx_mid, weight, bias, tau, dz_num, ds, dot, stats_in=N
             torch.empty(x_mid.shape, device=x.device, dtype=dt)
         dfx = torch.empty_like(fx_mid, dtype=dt) if fx_mid.stride(3) == 1 else \
             torch.empty(fx_mid.shape, device=x.device, dtype=dt)
-        dz = _small(dz_num, (call.B, H, call.G, DV), "dz_num")
-        dsv = _small(ds, (call.B, H, call.G), "ds")
-        st_in = None if stats_in is None else _small(stats_in, (B, H, 2, N), "stats")
+        dz = _small(dz_num, (call.B, H, call.G, DV), "dz_num", x.device)
+        dsv = _small(ds, (call.B, H, call.G), "ds", x.device)
+        st_in = None if stats_in is None else _small(stats_in, (B, H, 2, N), "stats", x.device)
         dW, db, dtau = _param_grad_buffers(call)
         ws, nws = call.workspace(_hip.OP_SLICE_BWD)
         _hip.check(_hip.lib().fs_slice_bwd(
@@ -408,8 +458,9 @@ def _hip_deslice_bwd(x_mid, weight, bias, tau, tokens, d_out, dot, stats_in=None
         x, do = _as_points(x_mid, dt), _as_points(d_out, dt)
         dxm = torch.empty_like(x_mid, dtype=dt) if x_mid.stride(3) == 1 else \
             torch.empty(x_mid.shape, device=x.device, dtype=dt)
-        tok = _small(tokens, (B, H, call.G, DV), "tokens")
-        st_in = None if stats_in is None else _small(stats_in, (x_mid.shape[0], H, 2, N), "stats")
+        tok = _small(tokens, (B, H, call.G, DV), "tokens", x.device)
+        st_in = (None if stats_in is None
+                 else _small(stats_in, (x_mid.shape[0], H, 2, N), "stats", x.device))
         dtok = torch.empty(B, H, call.G, DV, device=x.device, dtype=torch.float32)
         dW, db, dtau = _param_grad_buffers(call)
         ws, nws = call.workspace(_hip.OP_DESLICE_BWD)

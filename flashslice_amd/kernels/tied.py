@@ -81,9 +81,9 @@ def _hip_tied_bwd(x_mid, fx_mid, weight, bias, tau, tokens, d_out, dz_num, ds, d
             torch.empty(x_mid.shape, device=x.device, dtype=dt)
         dfx = torch.empty_like(fx_mid, dtype=dt) if fx_mid.stride(3) == 1 else \
             torch.empty(fx_mid.shape, device=x.device, dtype=dt)
-        tok = _small(tokens, (B, H, call.G, DV), "tokens")
-        dz = _small(dz_num, (B, H, call.G, DV), "dz_num")
-        dsv = _small(ds, (B, H, call.G), "ds")
+        tok = _small(tokens, (B, H, call.G, DV), "tokens", x.device)
+        dz = _small(dz_num, (B, H, call.G, DV), "dz_num", x.device)
+        dsv = _small(ds, (B, H, call.G), "ds", x.device)
         dtok = torch.empty(B, H, call.G, DV, device=x.device, dtype=torch.float32)
         dW, db, dtau = _param_grad_buffers(call)
         ws, nws = call.workspace(_hip.OP_TIED_BWD)

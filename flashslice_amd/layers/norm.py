@@ -90,8 +90,10 @@ def _ln_setup(ctx, inputs, output):
 
 def _ln_grad(ctx, gy, gmean, grstd):
     x, weight, mean, rstd = ctx.saved_tensors
-    dx, dw, db = torch.ops.flashslice_layer.layer_norm_bwd(gy.contiguous(), x, weight, mean,
-                                                           rstd)
+    gy = gy.contiguous()
+    if gy.data_ptr() % 16:
+        gy = gy.clone()  # the kernels read rows as 16-byte words
+    dx, dw, db = torch.ops.flashslice_layer.layer_norm_bwd(gy, x, weight, mean, rstd)
     return dx, dw, db, None
 
 
@@ -108,7 +110,10 @@ class PointLayerNorm(nn.LayerNorm):
                 and self.bias is not None and self.weight.dtype == torch.float32
                 and len(self.normalized_shape) == 1 and C == self.normalized_shape[0]
                 and C % 4 == 0 and 4 <= C <= 2048 and x.numel() // C >= MIN_ROWS
-                and not torch.is_autocast_enabled())
+                and not torch.is_autocast_enabled()
+                # the kernels read rows as 16-byte words: a view whose storage
+                # offset is not a multiple of 4 floats takes nn.LayerNorm
+                and (not x.is_contiguous() or x.data_ptr() % 16 == 0))
 
     def forward(self, x):
         if self._hip_ok(x):

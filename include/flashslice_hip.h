@@ -82,8 +82,15 @@ typedef struct fs_slice_params {
    * than N (N sizes the launch; it is not read from the device). Served by
    * the whole-G family only, without statistics (stats_in / stats_out must
    * be NULL; fs_compute_stats refuses it): FS_ERR_UNSUPPORTED otherwise.
-   * No counterpart in the reference, whose ROADMAP.md:66-68 plans it. */
+   * No counterpart in the reference, whose ROADMAP.md:66-68 plans it.
+   * The library never reads the splits on the host (that would synchronise):
+   * the kernels clamp every split to [0, total_rows] and every sample to N
+   * rows, so malformed splits give wrong sums but no access outside the
+   * point tensors' total_rows rows. */
   const int64_t* row_splits;
+  /* Rows of every point tensor of a ragged batch (>= 1 with row_splits;
+   * ignored without). */
+  int64_t total_rows;
 } fs_slice_params;
 
 /* Bytes of workspace an op needs for this shape (op: enum fs_op). */

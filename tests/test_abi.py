@@ -173,6 +173,11 @@ def test_tied_and_row_splits_refused_before_launch():
     splits = torch.tensor([0, 60, 100], dtype=torch.int64)
     p, keep = _params(B=2)
     p.row_splits = splits.data_ptr()
+    # the rows of the point tensors bound the device-side clamp of the splits
+    rc = lib.fs_deslice_fwd(ctypes.byref(x), ctypes.byref(p), ctypes.c_void_p(buf.data_ptr()),
+                            None, None, ctypes.byref(x), None, 0, None)
+    assert rc == _hip.FS_ERR_INVALID and b"total_rows" in lib.fs_last_error()
+    p.total_rows = 100
     rc = lib.fs_slice_fwd(ctypes.byref(x), ctypes.byref(x), ctypes.byref(p), None,
                           ctypes.c_void_p(buf.data_ptr()), ctypes.c_void_p(buf.data_ptr()),
                           ctypes.c_void_p(buf.data_ptr()), None, 0, None)

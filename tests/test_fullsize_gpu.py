@@ -22,54 +22,115 @@ from flashslice_amd.kernels import fused_deslice, fused_slice
 pytestmark = pytest.mark.gpu
 
 FULL = [
-    # name, Case kwargs, order -- BASELINE.json configs 2, 3 and 4
-    ("c2", dict(B=1, N=1_000_000, H=8, D=32, G=32, mode="hgd"), "slice-first"),
-    ("c4", dict(B=4, N=262_144, H=8, D=32, DV=64, G=64, mode="bhgd"), "deslice-first"),
-    ("c3-g256", dict(B=1, N=1_000_000, H=8, D=32, G=256, mode="hgd"), "slice-first"),
+    # name, Case kwargs, order, dot -- BASELINE.json configs 2, 3 and 4
+    ("c2", dict(B=1, N=1_000_000, H=8, D=32, G=32, mode="hgd"), "slice-first", ""),
+    ("c4", dict(B=4, N=262_144, H=8, D=32, DV=64, G=64, mode="bhgd"), "deslice-first", ""),
+    ("c3-g256", dict(B=1, N=1_000_000, H=8, D=32, G=256, mode="hgd"), "slice-first", ""),
     # G = 1024 at a quarter of config 3's N keeps the float64 oracle's
     # N x H x G tensors within the GPU's memory
-    ("c3-g1024-n262144", dict(B=1, N=262_144, H=8, D=32, G=1024, mode="hgd"), "slice-first"),
+    ("c3-g1024-n262144", dict(B=1, N=262_144, H=8, D=32, G=1024, mode="hgd"), "slice-first",
+     ""),
+    # config 3's bf16 dot mode: x, fx, W, b in bf16 (reference
+    # bench/parity_ops.py:134-136), gated against eager on the same bf16 inputs
+    ("c3-g256-bf16", dict(B=1, N=1_000_000, H=8, D=32, G=256, mode="hgd"), "slice-first",
+     "bf16"),
+    ("c3-g1024-n262144-bf16", dict(B=1, N=262_144, H=8, D=32, G=1024, mode="hgd"),
+     "slice-first", "bf16"),
 ]
 
 
-@pytest.mark.parametrize("name,kw,order", FULL, ids=[c[0] for c in FULL])
-def test_full_size_parity(name, kw, order):
+@pytest.mark.parametrize("name,kw,order,dot", FULL, ids=[c[0] for c in FULL])
+def test_full_size_parity(name, kw, order, dot):
     case = Case(**kw)
-    fails, rows = check_case(case, order=order, ref_device="cuda")
+    fails, rows = check_case(case, order=order, ref_device="cuda", dot=dot,
+                             blocked=kw["G"] > 128)
     print("\ncase %s" % name, flush=True)
     for k, ee, ef, fe in rows:
         print("  %-10s eager %.3e  fused %.3e  fused-vs-eager %.3e" % (k, ee, ef, fe))
     assert not fails, "\n".join(fails)
+    if dot:
+        # fused vs eager-on-bf16-inputs within 2e-2 wherever eager itself is
+        # within 1e-2 of float64
+        bad = [(k, fe) for k, ee, ef, fe in rows if ee < 1e-2 and not fe <= 2e-2]
+        assert not bad, bad
 
 
-@pytest.mark.parametrize("G", [32, 256])
-def test_full_size_properties(G):
+# tolerances of the size-independent properties: fp32-accurate dots keep
+# them to rounding of fp32 sums; bf16 dots round w, tokens and the point
+# tensors to 8 significant bits
+_TOL = {"": dict(s=1e-6, const=1e-6, dtok=1e-6, zero=1e-4),
+        "bf16": dict(s=1e-3, const=1e-2, dtok=1e-2, zero=1e-2)}
+
+
+@pytest.mark.parametrize("G,dot", [(32, ""), (256, ""), (1024, ""), (256, "bf16"),
+                                   (1024, "bf16")],
+                         ids=["g32", "g256", "g1024", "g256-bf16", "g1024-bf16"])
+def test_full_size_properties(G, dot):
+    from flashslice_amd.kernels import set_dot_mode
+    tol = _TOL[dot]
     torch.manual_seed(3)
     B, N, H, D = 1, 1_000_000, 8, 32
     dev = "cuda"
-    x = torch.randn(B, N, H, D, device=dev)
-    fx = torch.randn(B, N, H, D, device=dev)
+    pdt = torch.bfloat16 if dot else torch.float32
+    x = torch.randn(B, N, H, D, device=dev).to(pdt)
+    fx = torch.randn(B, N, H, D, device=dev).to(pdt)
     w = (torch.randn(H, G, D) / D ** 0.5).to(dev).requires_grad_(True)
     b = (0.02 * torch.randn(H, G)).to(dev).requires_grad_(True)
     tau = (0.3 + 0.7 * torch.rand(H)).to(dev)
-    # weights of every point sum to one: sum_g s = N for every (b, h)
-    z, s, st = fused_slice(x, fx, w, b, tau, return_stats=True)
-    tot = s.double().sum(-1)
-    assert torch.allclose(tot, torch.full_like(tot, float(N)), rtol=1e-6, atol=0), tot
-    # constant tokens deslice to themselves, point by point
-    c = torch.randn(B, H, 1, D, device=dev)
-    out = fused_deslice(x, w, b, tau, c.expand(B, H, G, D).contiguous(), stats=st)
-    ref = c[:, :, 0, :].unsqueeze(1).expand_as(out)
-    err = ((out - ref).norm() / ref.norm()).item()
-    assert err < 1e-6, err
-    # dtokens summed over slots = d_out summed over points; db and dW sum to
-    # zero over the slots (sum_g Lb = 0 for every point)
-    tok = torch.randn(B, H, G, D, device=dev, requires_grad=True)
-    out = fused_deslice(x, w, b, tau, tok, stats=st)
-    d_out = torch.randn_like(out)
-    gt, gw, gb = torch.autograd.grad((out * d_out).sum(), [tok, w, b])
+    set_dot_mode(dot)
+    try:
+        # weights of every point sum to one: sum_g s = N for every (b, h)
+        z, s, st = fused_slice(x, fx, w, b, tau, return_stats=True)
+        tot = s.double().sum(-1)
+        assert torch.allclose(tot, torch.full_like(tot, float(N)), rtol=tol["s"], atol=0), tot
+        # constant tokens deslice to themselves, point by point
+        c = torch.randn(B, H, 1, D, device=dev)
+        out = fused_deslice(x, w, b, tau, c.expand(B, H, G, D).contiguous(), stats=st)
+        ref = c[:, :, 0, :].unsqueeze(1).expand_as(out)
+        err = ((out.float() - ref).norm() / ref.norm()).item()
+        assert err < tol["const"], err
+        # dtokens summed over slots = d_out summed over points; db and dW sum
+        # to zero over the slots (sum_g Lb = 0 for every point)
+        tok = torch.randn(B, H, G, D, device=dev, requires_grad=True)
+        out = fused_deslice(x, w, b, tau, tok, stats=st)
+        d_out = torch.randn_like(out)
+        gt, gw, gb = torch.autograd.grad((out.float() * d_out.float()).sum(), [tok, w, b])
+    finally:
+        set_dot_mode("")
     lhs = gt.double().sum(2)                       # (B, H, D)
     rhs = d_out.double().sum(1)                    # (B, H, D)
-    assert ((lhs - rhs).norm() / rhs.norm()).item() < 1e-6
-    assert (gb.double().sum(-1).abs().max() / gb.double().abs().max()).item() < 1e-4
-    assert (gw.double().sum(1).norm() / gw.double().norm()).item() < 1e-4
+    assert ((lhs - rhs).norm() / rhs.norm()).item() < tol["dtok"]
+    assert (gb.double().sum(-1).abs().max() / gb.double().abs().max()).item() < tol["zero"]
+    assert (gw.double().sum(1).norm() / gw.double().norm()).item() < tol["zero"]
+
+
+def test_no_nhg_allocation_c3_g1024():
+    """The discriminative form of "no N x H x G allocation": at config 3's
+    G = 1024 (N = 1e6, H = 8) one such fp32 tensor is 32.8 GB, against ~1 GB
+    per point tensor. A full coupling step (forward and backward through the
+    public API and autograd) must peak far below it."""
+    torch.manual_seed(5)
+    B, N, H, D, G = 1, 1_000_000, 8, 32, 1024
+    dev = "cuda"
+    x = torch.randn(B, N, H, D, device=dev, requires_grad=True)
+    fx = torch.randn(B, N, H, D, device=dev, requires_grad=True)
+    w = (torch.randn(H, G, D) / D ** 0.5).to(dev).requires_grad_(True)
+    b = (0.02 * torch.randn(H, G)).to(dev).requires_grad_(True)
+    tau = (0.3 + 0.7 * torch.rand(H)).to(dev).requires_grad_(True)
+    d_out = torch.randn(B, N, H, D, device=dev)
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    z, s, st = fused_slice(x, fx, w, b, tau, return_stats=True)
+    out = fused_deslice(x, w, b, tau, z / (s + 1e-5)[..., None], stats=st)
+    (out * d_out).sum().backward()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated() - base
+    nhg = B * N * H * G * 4
+    xsz = B * N * H * D * 4
+    print("\npeak above inputs %.2f GB; one N x H x G fp32 tensor %.1f GB; one x %.2f GB"
+          % (peak / 1e9, nhg / 1e9, xsz / 1e9), flush=True)
+    assert peak < nhg / 4, peak
+    # out, dx (two ops + their sum), dfx and the grads: a handful of x-sized
+    # tensors plus statistics and partials
+    assert peak < 8 * xsz, peak
