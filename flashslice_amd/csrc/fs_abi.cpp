@@ -10,9 +10,11 @@
 #include <initializer_list>
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/flashslice_hip.h"
@@ -427,10 +429,22 @@ int32_t fs_compute_stats(const fs_points* x, const fs_slice_params* p, float* st
   return run_stats(x, p, stats, two_pass ? 1 : 0, a, st, who);
 }
 
-int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_params* p,
-                     const float* stats_in, float* stats_out, float* z_num, float* s,
-                     void* workspace, size_t workspace_bytes, void* stream) {
-  const char* who = "fs_slice_fwd";
+}  // extern "C"
+
+// Scratch of fs_slice_fwd_static: one copy per GPU the library runs on, held
+// until the process ends; every call on a GPU shares it. Nothing in it needs
+// to start at zero: the slice forward writes every partial (and statistic)
+// it later reads, as with a fresh, uninitialised workspace.
+constexpr size_t kScratchBytes = FS_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+// The slice forward on a given workspace: fs_slice_fwd (caller's buffer) and
+// fs_slice_fwd_static (the library's scratch array) share it.
+int32_t slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_params* p,
+                  const float* stats_in, float* stats_out, float* z_num, float* s,
+                  void* workspace, size_t workspace_bytes, void* stream, const char* who) {
   int32_t rc = check_params(p, who);
   if (!rc) rc = check_points(x, "x_mid", p->D, who);
   if (!rc) rc = check_points(fx, "fx_mid", p->DV, who);
@@ -490,6 +504,66 @@ int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_par
   rs.seg[1] = seg(ws.part, wf, (int64_t)G * DV, np, G, (int)p->B, (int)p->H, s);
   rs.n = 2;
   return hip_check(fs::launch_reduce((int)p->B, (int)p->H, rs, st), who);
+}
+
+// Device address of `scratch` per device, looked up once per device with
+// that device current (hipGetSymbolAddress: in host code the array's name
+// is not a device address).
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int32_t scratch_of_current_device(void** out, const char* who) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(FS_ERR_HIP, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(FS_ERR_UNSUPPORTED, "%s: device %d is beyond the %d this library serves", who, dev,
+                kMaxDevices);
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!ptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!ptr) {
+      e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !ptr)
+        return fail(FS_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev,
+                    hipGetErrorString(e));
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return FS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_params* p,
+                     const float* stats_in, float* stats_out, float* z_num, float* s,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  return slice_fwd(x, fx, p, stats_in, stats_out, z_num, s, workspace, workspace_bytes, stream,
+                   "fs_slice_fwd");
+}
+
+int32_t fs_slice_fwd_static(const fs_points* x, const fs_points* fx, const fs_slice_params* p,
+                            const float* stats_in, float* stats_out, float* z_num, float* s,
+                            void* stream) {
+  const char* who = "fs_slice_fwd_static";
+  int32_t rc = check_params(p, who);
+  if (rc) return rc;
+  const size_t need = plan_ws(FS_OP_SLICE_FWD, p, nullptr).bytes;
+  if (need > kScratchBytes)
+    return fail(FS_ERR_WORKSPACE,
+                "%s: this shape needs %zu bytes of scratch, the library's static buffer holds "
+                "%zu; call fs_slice_fwd with a workspace", who, need, kScratchBytes);
+  void* ptr = nullptr;
+  if (need > 0) {
+    rc = scratch_of_current_device(&ptr, who);
+    if (rc) return rc;
+  }
+  return slice_fwd(x, fx, p, stats_in, stats_out, z_num, s, ptr, kScratchBytes, stream, who);
 }
 
 int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float* tokens,

@@ -23,7 +23,7 @@ _DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 #: every entry point the header declares
 EXPORTS = ("fs_workspace_bytes", "fs_compute_stats", "fs_slice_fwd", "fs_deslice_fwd",
            "fs_slice_bwd", "fs_deslice_bwd", "fs_tied_bwd", "fs_family", "fs_last_error",
-           "fs_version",
+           "fs_version", "fs_slice_fwd_static",
            # the layer around the path (include/flashslice_layer.h)
            "fs_layernorm_fwd", "fs_layernorm_bwd", "fs_layernorm_workspace_bytes")
 
@@ -62,12 +62,13 @@ def _declare(lib):
     lib.fs_workspace_bytes.restype = S
     lib.fs_compute_stats.argtypes = [pts, prm, V, I32, V, S, V]
     lib.fs_slice_fwd.argtypes = [pts, pts, prm, V, V, V, V, V, S, V]
+    lib.fs_slice_fwd_static.argtypes = [pts, pts, prm, V, V, V, V, V]
     lib.fs_deslice_fwd.argtypes = [pts, prm, V, V, V, pts, V, S, V]
     lib.fs_slice_bwd.argtypes = [pts, pts, prm, V, V, V, pts, pts, V, V, V, V, S, V]
     lib.fs_deslice_bwd.argtypes = [pts, prm, V, V, pts, pts, V, V, V, V, V, S, V]
     lib.fs_tied_bwd.argtypes = [pts, pts, pts, prm, V, V, V, pts, pts, V, V, V, V, V, S, V]
     for name in ("fs_compute_stats", "fs_slice_fwd", "fs_deslice_fwd", "fs_slice_bwd",
-                 "fs_deslice_bwd", "fs_tied_bwd"):
+                 "fs_deslice_bwd", "fs_tied_bwd", "fs_slice_fwd_static"):
         getattr(lib, name).restype = I32
     lib.fs_family.argtypes = [prm]
     lib.fs_family.restype = I32

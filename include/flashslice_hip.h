@@ -112,6 +112,25 @@ int32_t fs_slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_par
                      const float* stats_in, float* stats_out, float* z_num, float* s,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of the static scratch array fs_slice_fwd_static uses (32 MiB). */
+#define FS_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* fs_slice_fwd without a workspace argument: it allocates nothing (no
+ * hipMalloc, hipFree or allocating library call), for callers that cannot
+ * allocate -- code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc. No counterpart in the reference. The partials (and
+ * the statistics the G-blocked kernels form when none are handed in) live in
+ * a file-scope device array of FS_SCRATCH_BYTES, one per GPU the library
+ * runs on, held until the process ends; its address is looked up once per
+ * device on the first call there. Shapes whose workspace
+ * (fs_workspace_bytes(FS_OP_SLICE_FWD, p)) exceeds it return
+ * FS_ERR_WORKSPACE before any launch. Results are bitwise equal to
+ * fs_slice_fwd's. Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (two streams, or two threads without ordering) race. */
+int32_t fs_slice_fwd_static(const fs_points* x, const fs_points* fx, const fs_slice_params* p,
+                            const float* stats_in, float* stats_out, float* z_num, float* s,
+                            void* stream);
+
 /* Replaces flashslice::flash_deslice (_deslice_impl, slice_ops.py:846-859)
  * and flashslice::deslice_blk (_deslice_blk_impl, blocked.py:1406-1433):
  * out (B, N, H, DV) in the point dtype from tokens (B, H, G, DV) fp32. */
