@@ -508,7 +508,7 @@ def bench_model(a, cfg):
     check (two steps, bitwise equal loss and gradients), peak memory, then K
     timed steps; the CPU baseline is the same model on its eager route on a
     bounded sample of points."""
-    from flashslice_amd.layers import Transolver
+    from flashslice_amd.models import Transolver
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     kw = {k: cfg[k] for k in ("space_dim", "fun_dim", "out_dim", "n_hidden", "n_heads",

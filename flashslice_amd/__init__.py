@@ -20,7 +20,10 @@ __all__ = list(_LAYER_NAMES) + ["__version__"]
 
 
 def __getattr__(name):
-    if name in _LAYER_NAMES:
+    if name == "Physics_Attention_Irregular_Mesh":
         from . import layers
-        return getattr(layers, name)
+        return layers.Physics_Attention_Irregular_Mesh
+    if name in _LAYER_NAMES:
+        from . import models
+        return getattr(models, name)
     raise AttributeError("module 'flashslice_amd' has no attribute %r" % name)

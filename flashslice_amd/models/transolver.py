@@ -21,9 +21,9 @@ import torch
 import torch.nn as nn
 from torch.nn.init import trunc_normal_
 
-from .basic import MLP, PointLinear
-from .norm import PointLayerNorm
-from .physics_attention import TOKEN_EPS, Physics_Attention_Irregular_Mesh
+from ..layers.basic import MLP, PointLinear
+from ..layers.norm import PointLayerNorm
+from ..layers.physics_attention import TOKEN_EPS, Physics_Attention_Irregular_Mesh
 
 
 class TransolverBlock(nn.Module):

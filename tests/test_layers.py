@@ -8,8 +8,8 @@ import pytest
 import torch
 
 import oracle
-from flashslice_amd.layers import (MLP, Physics_Attention_Irregular_Mesh, Transolver,
-                                   TransolverBlock)
+from flashslice_amd.layers import MLP, Physics_Attention_Irregular_Mesh
+from flashslice_amd.models import Transolver, TransolverBlock
 from flashslice_amd.layers.physics_attention import TOKEN_EPS
 
 
@@ -173,8 +173,8 @@ def test_package_root_exports_the_models():
     """``from flashslice_amd import Transolver`` as the reference's
     ``from flashslice import Transolver`` (reference flashslice/__init__.py:18-27)."""
     import flashslice_amd
-    from flashslice_amd import layers
-    for name in ("Transolver", "TransolverBlock", "TokenTransformerBlock",
-                 "Physics_Attention_Irregular_Mesh"):
-        assert getattr(flashslice_amd, name) is getattr(layers, name)
+    from flashslice_amd import layers, models
+    for name in ("Transolver", "TransolverBlock", "TokenTransformerBlock"):
+        assert getattr(flashslice_amd, name) is getattr(models, name)
+    assert flashslice_amd.Physics_Attention_Irregular_Mesh is layers.Physics_Attention_Irregular_Mesh
     assert flashslice_amd.__version__

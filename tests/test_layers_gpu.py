@@ -26,7 +26,8 @@ import pytest
 import torch
 
 from parity import relerr
-from flashslice_amd.layers import Physics_Attention_Irregular_Mesh, Transolver
+from flashslice_amd.layers import Physics_Attention_Irregular_Mesh
+from flashslice_amd.models import Transolver
 from flashslice_amd.layers.basic import PointLinear
 from flashslice_amd.layers.norm import PointLayerNorm
 
