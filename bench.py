@@ -37,6 +37,7 @@ import functools
 import json
 import os
 import sys
+import subprocess
 import time
 
 import torch
@@ -226,6 +227,72 @@ def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", dot=0
     ds = dsb - (dtok * tok).sum(-1) / den[..., 0]
     dx2, dfx, dW2, db2, dt2 = timed("slice_bwd", slice_b, st, dz, ds)
     return z, s, out, dx1, dtok, dW1, db1, dt1, dx2, dfx, dW2, db2, dt2
+
+
+def public_step(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order, coupling):
+    """The coupling step as a user writes it: the public API on leaves that
+    require grad, and autograd for the backward (its host cost, and for the
+    two plain ops the sum of their two dx, included). slice-first: tokens =
+    z / (s + eps); deslice-first: the given tokens are deslided and the
+    slice pools fx = tanh(out), a pointwise stand-in for the MLP of the
+    deslice -> MLP -> slice chain (its dfx must reach the step's backward
+    before the deslice's backward). ``coupling``: ``fused_coupling`` (merged
+    backward) instead of the two plain ops. Returns the leaves' gradients."""
+    from flashslice_amd.kernels import fused_coupling, fused_deslice, fused_slice
+    x, fx, W, b, tau, tok0 = [t.detach().requires_grad_(True) for t in (x, fx, W, b, tau, tok0)]
+    if coupling:
+        c = fused_coupling(x, W, b, tau)
+        slice_, deslice_ = c.slice, c.deslice
+    else:
+        slice_ = lambda f: fused_slice(x, f, W, b, tau)  # noqa: E731
+        deslice_ = lambda t: fused_deslice(x, W, b, tau, t)  # noqa: E731
+    if order == "slice-first":
+        z, s = slice_(fx)
+        out = deslice_(z / (s + EPS)[..., None])
+        want = [x, fx, W, b, tau]
+    else:
+        out = deslice_(tok0)
+        z, s = slice_(torch.tanh(out))
+        want = [x, W, b, tau, tok0]
+    return torch.autograd.grad([out, z, s], want, [d_out, dzb, dsb])
+
+
+def time_public(inputs, order, steps, warmup):
+    """Median ms per step of ``public_step`` with the two plain ops and with
+    ``fused_coupling``, and the largest relative difference of their
+    gradients."""
+    res = {}
+    grads = {}
+    for name, cp in (("two_ops", False), ("coupling", True)):
+        for _ in range(warmup):
+            public_step(*inputs, order, cp)
+        grads[name] = public_step(*inputs, order, cp)
+        ts = []
+        for _ in range(steps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            public_step(*inputs, order, cp)
+            e1.record()
+            ts.append((e0, e1))
+        torch.cuda.synchronize()
+        ms = sorted(e0.elapsed_time(e1) for e0, e1 in ts)
+        res[name + "_ms"] = round(ms[len(ms) // 2], 4)
+    diff = max(float((u.double() - v.double()).norm() / v.double().norm().clamp_min(1e-30))
+               for u, v in zip(grads["coupling"], grads["two_ops"]))
+    res["coupling_vs_two_ops_relerr"] = float("%.3e" % diff)
+    return res
+
+
+def cpu_model():
+    """The host CPU's model name (lscpu), for the CPU baseline's record."""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return None
 
 
 def cpu_baseline(B, N, H, D, DV, G, layout, order, budget_s=20.0):
@@ -723,7 +790,18 @@ def main():
         cpu = {"value": round(v / 1e6, 4), "unit": "Mpoints/s", "cores": thr, "kind": "port",
                "sample": "eager PyTorch softmax/einsum oracle (oracle/eager.py), fp32 fwd+bwd "
                          "of the same coupling on %d of the %d points, median of 3 runs, "
-                         "torch threads=%d, os.cpu_count()=%d" % (n_s, N, thr, os.cpu_count())}
+                         "torch threads=%d, os.cpu_count()=%d" % (n_s, N, thr, os.cpu_count()),
+               "cpu_model": cpu_model()}
+
+    # the same step through the public API and autograd: the two plain ops
+    # against the coupling with the merged backward (deslice-first with an
+    # MLP between the ops: the deslice -> MLP -> slice chain)
+    public = None
+    if a.dot == "ieee":
+        public = time_public(inputs, order, a.steps, max(2, a.warmup))
+        public["step"] = ("slice -> z/(s+eps) -> deslice" if order == "slice-first" else
+                          "deslice -> fx = tanh(out) -> slice")
+        public["includes"] = "host cost per op call, autograd (the two ops' dx sum)"
 
     line = {
         "metric": "slice+deslice fwd+bwd Mpoints/s at N=1M,H=8,D=32,G=32 (ms and peak HBM "
@@ -756,6 +834,7 @@ def main():
         "peak_hbm_gb": round(peak_gb, 3),
         "nxhxg_gb": round(B * N * H * G * 4 / 1e9, 3),
         "deterministic": deterministic,
+        "public_api": public,
         "cpu_baseline": cpu,
     }
     line["roofline"].update({

@@ -5,7 +5,7 @@
     from flashslice.kernels import fused_slice, fused_deslice, unsupported_dims
 
 ``flashslice`` and its submodules -- ``kernels`` (``slice_ops``,
-``blocked``, plus this build's ``tied`` and ``varlen``), ``layers``
+``blocked``, plus this build's ``tied``, ``coupling`` and ``varlen``), ``layers``
 (``basic``, ``physics_attention``, ``norm``) and ``models``
 (``transolver``) -- are bound to the modules of ``flashslice_amd``, the
 package that holds the HIP operators. They are the same module objects, not
@@ -21,7 +21,7 @@ import sys
 import flashslice_amd as _impl
 
 _SUBMODULES = ("kernels", "kernels.slice_ops", "kernels.blocked", "kernels.tied",
-               "kernels.varlen", "layers", "layers.basic", "layers.physics_attention",
+               "kernels.coupling", "kernels.varlen", "layers", "layers.basic", "layers.physics_attention",
                "layers.norm", "models", "models.transolver")
 
 for _name in _SUBMODULES:

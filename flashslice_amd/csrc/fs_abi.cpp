@@ -798,14 +798,16 @@ int32_t fs_tied_bwd(const fs_points* x, const fs_points* fx, const fs_points* d_
   if (!rc) rc = check_points(fx, "fx_mid", p->DV, who);
   if (!rc) rc = check_points(d_out, "d_out", p->DV, who);
   if (!rc) rc = check_out_points(dx, "dx", p->D, who);
-  if (!rc) rc = check_out_points(dfx, "dfx", p->DV, who);
+  // dfx may be NULL (or have a NULL data pointer): not written
+  const bool want_dfx = dfx && dfx->data;
+  if (!rc && want_dfx) rc = check_out_points(dfx, "dfx", p->DV, who);
   if (rc) return rc;
   if (fx->dtype != x->dtype || d_out->dtype != x->dtype || dx->dtype != x->dtype ||
-      dfx->dtype != x->dtype)
+      (want_dfx && dfx->dtype != x->dtype))
     return fail(FS_ERR_INVALID, "%s: point tensors must share one dtype", who);
-  if (!tokens || !dz_num || !ds || !dtokens || !dweight || !dbias || !dtau)
+  if (!tokens || !dz_num || !ds || !dweight || !dbias || !dtau)
     return fail(FS_ERR_INVALID,
-                "%s: tokens, dz_num, ds, dtokens, dweight, dbias, dtau must be non-NULL", who);
+                "%s: tokens, dz_num, ds, dweight, dbias, dtau must be non-NULL", who);
   if (family_of(p) != 1)
     return fail(FS_ERR_UNSUPPORTED,
                 "%s: served by the whole-G kernels only (G <= 128 and D, DV small enough); "
@@ -828,11 +830,11 @@ int32_t fs_tied_bwd(const fs_points* x, const fs_points* fx, const fs_points* d_
   set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
   set_in(d_out, &a.g, &a.sgb, &a.sgn, &a.sgh);
   set_out(dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
-  set_out(dfx, &a.o2, &a.s2b, &a.s2n, &a.s2h);
+  if (want_dfx) set_out(dfx, &a.o2, &a.s2b, &a.s2n, &a.s2h);
   a.vec_x = vec_ok(x);
   a.vec_f = vec_ok(fx) && vec_ok(d_out);
   a.vec_1 = vec_ok(dx);
-  a.vec_2 = vec_ok(dfx);
+  a.vec_2 = want_dfx ? vec_ok(dfx) : 1;
   a.fast = a.vec_x && a.vec_f && a.vec_1 && a.vec_2 && full_widths(p);
   a.tok = dz_num;
   a.tok2 = tokens;
@@ -842,11 +844,12 @@ int32_t fs_tied_bwd(const fs_points* x, const fs_points* fx, const fs_points* d_
   rc = hip_check(fs::launch_fused_tied_bwd(a, x->dtype, mode, st), who);
   if (rc) return rc;
   fs::ReduceSegments rs{};
-  rs.seg[0] = seg(ws.part, wf, 0, pb(g), G * DV, (int)p->B, (int)p->H, dtokens);
-  rs.seg[1] = seg(ws.part, wf, offW, pb(g), G * D, Bw, Hw, dweight);
-  rs.seg[2] = seg(ws.part, wf, offB, pb(g), G, Bb, Hb, dbias);
-  rs.seg[3] = seg(ws.part, wf, offB + G, pb(g), 1, 1, (int)p->H, dtau);
-  rs.n = 4;
+  rs.n = 0;
+  // dtokens may be NULL: not reduced
+  if (dtokens) rs.seg[rs.n++] = seg(ws.part, wf, 0, pb(g), G * DV, (int)p->B, (int)p->H, dtokens);
+  rs.seg[rs.n++] = seg(ws.part, wf, offW, pb(g), G * D, Bw, Hw, dweight);
+  rs.seg[rs.n++] = seg(ws.part, wf, offB, pb(g), G, Bb, Hb, dbias);
+  rs.seg[rs.n++] = seg(ws.part, wf, offB + G, pb(g), 1, 1, (int)p->H, dtau);
   return hip_check(fs::launch_reduce((int)p->B, (int)p->H, rs, st), who);
 }
 

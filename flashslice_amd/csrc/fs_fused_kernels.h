@@ -637,7 +637,8 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
               o[vb] = mma<MV>(wq, zq, o[vb]);
             }
           }
-          const Rsrc rdf = rows_rsrc_sel(df_b, df_sn, df_w, p0, N);
+          // no dfx wanted (a.o2 null): an empty range drops every store
+          const Rsrc rdf = rows_rsrc_sel(df_b, df_sn, df_w, p0, a.o2 ? N : 0);
 #pragma unroll
           for (int vb = 0; vb < NVB; ++vb) st_cols<T>(rdf, vcf[vb], (uint32_t)df_sn, o[vb]);
         }
@@ -1056,7 +1057,8 @@ __global__ __launch_bounds__(256, (NGB * NDB * NVB == 1) ? 2 : 1) void k_fused_t
               o[vb] = mma<MV>(wq, zq, o[vb]);
             }
           }
-          const Rsrc rdf = rows_rsrc_sel(df_b, df_sn, df_w, p0, N);
+          // no dfx wanted (a.o2 null): an empty range drops every store
+          const Rsrc rdf = rows_rsrc_sel(df_b, df_sn, df_w, p0, a.o2 ? N : 0);
 #pragma unroll
           for (int vb = 0; vb < NVB; ++vb) st_cols<T>(rdf, vcf[vb], (uint32_t)df_sn, o[vb]);
         }

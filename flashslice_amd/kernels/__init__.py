@@ -10,7 +10,9 @@ implementation.
 
 The eleven public names are those of the reference package
 (``flashslice/kernels/__init__.py:44-59``). Additions: ``fused_deslice_slice``
-(a deslice -> slice coupling with one fused backward pass, ``tied.py``) and
+(a deslice -> slice coupling with one fused backward pass, ``tied.py``),
+``fused_coupling`` (a slice/deslice coupling in either order with any step
+between the two ops, its backward merged into one pass, ``coupling.py``) and
 ``fused_slice_varlen`` / ``fused_deslice_varlen`` (ragged batches through
 row splits, ``varlen.py``).
 """
@@ -28,9 +30,10 @@ from .slice_ops import (
 from . import blocked  # noqa: F401  -- registers the flashslice::*_blk ops
 from .blocked import set_block_g, set_stats_mode, stats_mode
 from .tied import fused_deslice_slice
+from .coupling import fused_coupling
 from .varlen import fused_deslice_varlen, fused_slice_varlen
 
 __all__ = ["fused_slice", "fused_deslice", "unsupported_dims", "single_tile_dims",
            "set_dot_mode", "set_kernel_mode", "set_block_g", "set_stats_mode",
            "stats_mode", "set_tile_table", "tile_table", "fused_deslice_slice",
-           "fused_slice_varlen", "fused_deslice_varlen"]
+           "fused_coupling", "fused_slice_varlen", "fused_deslice_varlen"]

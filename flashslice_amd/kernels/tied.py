@@ -64,9 +64,11 @@ def _deslice_slice_impl(x_mid, fx_mid, weight, bias, tau, tokens, dot):
     return out, z_num, s
 
 
-def _hip_tied_bwd(x_mid, fx_mid, weight, bias, tau, tokens, d_out, dz_num, ds, dot):
+def _hip_tied_bwd(x_mid, fx_mid, weight, bias, tau, tokens, d_out, dz_num, ds, dot,
+                  want_dfx=True, want_dtok=True):
     """Both ops' gradients from fs_tied_bwd; None where the whole-G kernels
-    do not serve the shape."""
+    do not serve the shape. ``want_dfx`` / ``want_dtok`` False: that output
+    is not formed (None in its place)."""
     B, N, H, D = x_mid.shape
     DV = fx_mid.shape[3]
     with torch.cuda.device(x_mid.device):
@@ -79,25 +81,28 @@ def _hip_tied_bwd(x_mid, fx_mid, weight, bias, tau, tokens, d_out, dz_num, ds, d
         x, fx, do = _as_points(x_mid, dt), _as_points(fx_mid, dt), _as_points(d_out, dt)
         dxm = torch.empty_like(x_mid, dtype=dt) if x_mid.stride(3) == 1 else \
             torch.empty(x_mid.shape, device=x.device, dtype=dt)
-        dfx = torch.empty_like(fx_mid, dtype=dt) if fx_mid.stride(3) == 1 else \
-            torch.empty(fx_mid.shape, device=x.device, dtype=dt)
+        dfx = None
+        if want_dfx:
+            dfx = torch.empty_like(fx_mid, dtype=dt) if fx_mid.stride(3) == 1 else \
+                torch.empty(fx_mid.shape, device=x.device, dtype=dt)
         tok = _small(tokens, (B, H, call.G, DV), "tokens", x.device)
         dz = _small(dz_num, (B, H, call.G, DV), "dz_num", x.device)
         dsv = _small(ds, (B, H, call.G), "ds", x.device)
-        dtok = torch.empty(B, H, call.G, DV, device=x.device, dtype=torch.float32)
+        dtok = (torch.empty(B, H, call.G, DV, device=x.device, dtype=torch.float32)
+                if want_dtok else None)
         dW, db, dtau = _param_grad_buffers(call)
         ws, nws = call.workspace(_hip.OP_TIED_BWD)
         _hip.check(_hip.lib().fs_tied_bwd(
             _hip.points(x, D), _hip.points(fx, DV), _hip.points(do, DV), call.prm,
             _hip.ptr(tok), _hip.ptr(dz), _hip.ptr(dsv), _hip.points(dxm, D),
-            _hip.points(dfx, DV), _hip.ptr(dtok), _hip.ptr(dW), _hip.ptr(db), _hip.ptr(dtau),
-            _hip.ptr(ws), nws, call.stream()))
+            _hip.points(dfx, DV) if want_dfx else None, _hip.ptr(dtok), _hip.ptr(dW),
+            _hip.ptr(db), _hip.ptr(dtau), _hip.ptr(ws), nws, call.stream()))
     if dxm.dtype != x_mid.dtype:
         dxm = dxm.to(x_mid.dtype)
-    if dfx.dtype != fx_mid.dtype:
+    if dfx is not None and dfx.dtype != fx_mid.dtype:
         dfx = dfx.to(fx_mid.dtype)
     return ((dxm, dfx) + _grads_out(call, weight, bias, tau, dW, db, dtau)
-            + (dtok.to(tokens.dtype),))
+            + (None if dtok is None else dtok.to(tokens.dtype),))
 
 
 def _deslice_slice_bwd_impl(x_mid, fx_mid, weight, bias, tau, tokens, d_out, dz_num, ds, dot):

@@ -167,7 +167,11 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
  * back on the same saved inputs; it is the "tied backward fusion" of the
  * reference's ROADMAP.md:58-65, which the reference does not implement.
  * Served by the whole-G family only (fs_family() == 1); other shapes return
- * FS_ERR_UNSUPPORTED and the caller runs the two backward ops. */
+ * FS_ERR_UNSUPPORTED and the caller runs the two backward ops.
+ * dfx (or its data pointer) and dtokens may be NULL: that output is not
+ * written. A deslice -> MLP -> slice chain has formed dfx before the MLP's
+ * backward, and a slice -> deslice chain has formed dtokens before the token
+ * mixing's backward; the rest of both ops' backward is this one pass. */
 int32_t fs_tied_bwd(const fs_points* x, const fs_points* fx, const fs_points* d_out,
                     const fs_slice_params* p, const float* tokens, const float* dz_num,
                     const float* ds, const fs_points* dx, const fs_points* dfx,

@@ -132,6 +132,15 @@ def check_case(case, order="slice-first", dot="", kernel_mode="auto", gate=1.25,
     finally:
         set_dot_mode("")
         set_kernel_mode("auto")
+    return compare(ref, ea, fu, fu2, amp=amp, gate=gate, blocked=blocked, strict=strict)
+
+
+def compare(ref, ea, fu, fu2, amp=False, gate=1.25, blocked=False, strict=True):
+    """The gates of the module docstring on result dicts (name -> tensor) of
+    the float64 oracle (``ref``), eager fp32 (``ea``) and two runs of the
+    HIP path (``fu``, ``fu2``); ``amp``: the 16-bit dtype of the inputs, or
+    False. Returns (failures, rows of (name, eager err, fused err,
+    fused-vs-eager))."""
     fails, rows = [], []
     for k in ref:
         if k not in fu:

@@ -169,7 +169,7 @@ def test_public_api_names():
     assert set(K.__all__) == {"fused_slice", "fused_deslice", "unsupported_dims",
                               "single_tile_dims", "set_dot_mode", "set_kernel_mode",
                               "set_block_g", "set_stats_mode", "stats_mode", "set_tile_table",
-                              "tile_table", "fused_deslice_slice", "fused_slice_varlen",
+                              "tile_table", "fused_deslice_slice", "fused_coupling", "fused_slice_varlen",
                               "fused_deslice_varlen"}
     assert set(fb.__all__) == {"tiles", "set_block_g", "compute_stats", "set_stats_mode",
                                "stats_mode"}

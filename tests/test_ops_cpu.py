@@ -263,3 +263,85 @@ def test_varlen_device_splits_need_max_rows():
         fused_slice_varlen(x, x, w, b, tau, m(4, dtype=torch.int32), max_rows=50)
     z, s = fused_slice_varlen(x, x, w, b, tau, m(4, dtype=torch.int64), max_rows=50)
     assert z.shape == (3, 3, 5, 8) and s.shape == (3, 3, 5)
+
+
+# ------------------------------------------------- coupling with merged backward
+COUPLING_OPS = ("tied_deslice", "tied_slice_after", "tied_deslice_bwd", "tied_slice",
+                "tied_deslice_after", "tied_slice_bwd")
+
+
+def _coupling_meta(B=2, N=37, H=3, D=8, DV=12, G=5, dtype=torch.float32):
+    m = lambda *s, dt=torch.float32: torch.empty(  # noqa: E731
+        *s, device="meta", dtype=dt, requires_grad=True)
+    return (m(B, N, H, D, dt=dtype), m(B, N, H, DV, dt=dtype), m(B, H, G, D), m(H, G), m(H),
+            m(B, H, G, DV))
+
+
+def test_coupling_ops_registered():
+    for name in COUPLING_OPS:
+        assert hasattr(torch.ops.flashslice, name), name
+
+
+@pytest.mark.parametrize("order", ["deslice-first", "slice-first"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_coupling_fakes_and_autograd(order, dtype):
+    """fused_coupling in either order, with a differentiable step between the
+    ops: outputs with the plain ops' shapes and dtypes, and every leaf's
+    gradient in its shape and dtype (meta tensors: the fakes and the
+    hand-over through the links)."""
+    from flashslice_amd.kernels import fused_coupling
+    x, fx, w, b, tau, tok = _coupling_meta(dtype=dtype)
+    B, N, H, D = x.shape
+    G, DV = w.shape[-2], fx.shape[3]
+    lin = torch.empty(DV, DV, device="meta", requires_grad=True)
+    c = fused_coupling(x, w, b, tau)
+    if order == "deslice-first":
+        out = c.deslice(tok)
+        z, s = c.slice(torch.tanh(out.float() @ lin).to(dtype))
+    else:
+        z, s = c.slice(fx)
+        out = c.deslice((z / (s + 1e-5)[..., None]) @ lin)
+    assert out.shape == (B, N, H, DV) and out.dtype == dtype
+    assert z.shape == (B, H, G, DV) and z.dtype == torch.float32
+    assert s.shape == (B, H, G) and s.dtype == torch.float32
+    leaves = [x, w, b, tau, lin] + ([tok] if order == "deslice-first" else [fx])
+    gs = torch.autograd.grad(out.float().sum() + z.sum() + s.sum(), leaves)
+    assert [g.shape for g in gs] == [t.shape for t in leaves]
+    assert [g.dtype for g in gs] == [t.dtype for t in leaves]
+
+
+def test_coupling_misuse_refused():
+    from flashslice_amd.kernels import fused_coupling
+    x, fx, w, b, tau, tok = _coupling_meta(DV=12)
+    c = fused_coupling(x, w, b, tau)
+    c.deslice(tok)
+    with pytest.raises(RuntimeError, match="called twice"):
+        c.deslice(tok)
+    with pytest.raises(ValueError, match="value width 8"):
+        c.slice(torch.empty(2, 37, 3, 8, device="meta"))
+    c.slice(fx)
+    with pytest.raises(RuntimeError, match="one slice and one deslice"):
+        c.slice(fx)
+
+
+@pytest.mark.parametrize("order", ["deslice-first", "slice-first"])
+def test_coupling_compile_keeps_one_graph(order):
+    import torch._dynamo
+    from flashslice_amd.kernels import fused_coupling
+
+    def layer(x, fx, w, b, tau, tok, lin):
+        c = fused_coupling(x, w, b, tau)
+        if order == "deslice-first":
+            out = c.deslice(tok)
+            z, s = c.slice(torch.nn.functional.gelu(out @ lin))
+        else:
+            z, s = c.slice(fx)
+            out = c.deslice((z / (s + 1e-5)[..., None]) @ lin)
+        return out, z, s
+
+    torch._dynamo.reset()
+    m = lambda *s: torch.empty(*s, device="meta")  # noqa: E731
+    explain = torch._dynamo.explain(layer)(m(2, 37, 3, 8), m(2, 37, 3, 8), m(3, 5, 8), m(3, 5),
+                                           m(3), m(2, 3, 5, 8), m(8, 8))
+    assert explain.graph_break_count == 0, explain.break_reasons
+    assert explain.graph_count == 1
