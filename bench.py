@@ -353,14 +353,15 @@ def bench_ragged(a, cfg):
     nmax = max(lens)
 
     def ragged():
-        z, s = ops.slice_varlen(x, fx, W, b, tau, rs, nmax, 0)
+        z, s, st = ops.slice_varlen(x, fx, W, b, tau, rs, nmax, None, 0)
         den = (s + EPS)[..., None]
         tok = z / den
-        out = ops.deslice_varlen(x, W, b, tau, tok, rs, nmax, 0)
-        dx1, dtok, dW1, db1, dt1 = ops.deslice_varlen_bwd(x, W, b, tau, tok, rs, nmax, d_out, 0)
+        out, _ = ops.deslice_varlen(x, W, b, tau, tok, rs, nmax, st, 0)
+        dx1, dtok, dW1, db1, dt1 = ops.deslice_varlen_bwd(x, W, b, tau, tok, rs, nmax, st, d_out,
+                                                          0)
         dz = dzb + dtok / den
         ds = dsb - (dtok * tok).sum(-1) / den[..., 0]
-        dx2, dfx, dW2, db2, dt2 = ops.slice_varlen_bwd(x, fx, W, b, tau, rs, nmax, dz, ds, 0)
+        dx2, dfx, dW2, db2, dt2 = ops.slice_varlen_bwd(x, fx, W, b, tau, rs, nmax, st, dz, ds, 0)
         return z, s, out, dx1, dtok, dx2, dfx
 
     def looped():

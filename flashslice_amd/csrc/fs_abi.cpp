@@ -82,7 +82,15 @@ int64_t gp_blocks(GpGrid k, int dk) {
   }
 }
 
-Geo geo_gp(const fs_slice_params* p, GpGrid k, int dk) { return geo_n(p, gp_blocks(k, dk)); }
+constexpr int64_t kRaggedBlocksPerBH = 8;
+Geo geo_gp(const fs_slice_params* p, GpGrid k, int dk) {
+  int64_t t = gp_blocks(k, dk);
+  // a ragged batch: at least a few blocks per (sample, head), as the whole-G
+  // launches below
+  const int64_t rt = kRaggedBlocksPerBH * p->B * p->H;
+  if (p->row_splits && rt > t) t = rt;
+  return geo_n(p, t);
+}
 
 // slot-owned grids: the target is shared among the ceil(G / 32) slot blocks;
 // dk -1 sizes for the largest of the dot kinds (workspace planning)
@@ -103,7 +111,6 @@ Geo geo_g(const fs_slice_params* p, int dk) {
 // samples' tiles are spread over enough waves to keep the tail short
 // (measured on 64 meshes of N ~ U[2000, 40000]: 4.31 ms per step with the
 // plain targets, 4.20 / 3.67 / 3.75 ms with 4 / 8 / 16 blocks per pair).
-constexpr int64_t kRaggedBlocksPerBH = 8;
 int64_t fused_target(int32_t op, const fs_slice_params* p) {
   const bool one = p->G <= 32 && p->D <= 32 && p->DV <= 32;
   int64_t t;
@@ -239,35 +246,21 @@ fs::Args base_args(const fs_slice_params* p, const Geo& g) {
   return a;
 }
 
-// A ragged batch addresses sample b from its first row (row splits): the
-// point tensors' strides along b are not used.
-void ragged_strides(fs::Args& a) {
-  if (!a.rows) return;
-  a.sxb = a.sfb = a.s1b = a.s2b = a.sgb = 0;
-}
 
-// Row splits need the whole-G kernels and no statistics.
-int32_t check_rows(const fs_slice_params* p, const void* stats_in, const void* stats_out,
-                   const char* who) {
-  if (!p->row_splits) return FS_OK;
-  if (family_of(p) != 1)
-    return fail(FS_ERR_UNSUPPORTED,
-                "%s: row splits are served by the whole-G kernels only (G <= 128 and D, DV "
-                "small enough, family not forced to 2)", who);
-  if (stats_in || stats_out)
-    return fail(FS_ERR_UNSUPPORTED, "%s: statistics are not supported with row splits", who);
-  return FS_OK;
-}
 
-void set_in(const fs_points* t, const void** d, int64_t* sb, int64_t* sn, int64_t* sh) {
+// A point tensor's pointer and strides; a ragged batch addresses sample b
+// from its first row (row splits), so its stride along b is not used.
+void set_in(const fs_slice_params* p, const fs_points* t, const void** d, int64_t* sb,
+            int64_t* sn, int64_t* sh) {
   *d = t->data;
-  *sb = t->stride_b;
+  *sb = p->row_splits ? 0 : t->stride_b;
   *sn = t->stride_n;
   *sh = t->stride_h;
 }
-void set_out(const fs_points* t, void** d, int64_t* sb, int64_t* sn, int64_t* sh) {
+void set_out(const fs_slice_params* p, const fs_points* t, void** d, int64_t* sb, int64_t* sn,
+             int64_t* sh) {
   *d = t->data;
-  *sb = t->stride_b;
+  *sb = p->row_splits ? 0 : t->stride_b;
   *sn = t->stride_n;
   *sh = t->stride_h;
 }
@@ -300,6 +293,13 @@ bool gp_on(const fs_slice_params* p) { return fs::gp_serves((int)p->D, (int)p->D
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
+// Rows of one per-point buffer (delta, row sums; the statistics hold two
+// such): B * H planes of N points, or for a ragged batch H planes of its
+// total_rows rows (fs::rows_of).
+int64_t pt_rows(const fs_slice_params* p) {
+  return p->row_splits ? p->H * p->total_rows : p->B * p->H * p->N;
+}
+
 Workspace plan_ws(int32_t op, const fs_slice_params* p, char* base) {
   Workspace w;
   size_t off = 0;
@@ -327,10 +327,10 @@ Workspace plan_ws(int32_t op, const fs_slice_params* p, char* base) {
     w.part = take((size_t)(bh * pb(g) * wave_floats(op, p)));
   } else {
     const Geo gn = geo_gp(p, GPG_BWD_N, 0), gg = geo_g(p, -1);
-    w.stats = take((size_t)(bh * 2 * p->N));
+    w.stats = take((size_t)(pt_rows(p) * 2));
     if (op != FS_OP_SLICE_FWD) {
-      w.delta = take((size_t)(bh * p->N));
-      w.lsum = take((size_t)(bh * p->N));
+      w.delta = take((size_t)pt_rows(p));
+      w.lsum = take((size_t)pt_rows(p));
       w.part2 = take((size_t)(bh * gn.P));
     }
     w.part = take((size_t)(bh * gg.P * wave_floats(op, p)));
@@ -381,7 +381,7 @@ int32_t run_stats(const fs_points* x, const fs_slice_params* p, float* stats, in
                   const fs::Args& prepared, hipStream_t st, const char* who) {
   const Geo g = geo_gp(p, GPG_STATS, 0);
   fs::Args a = base_args(p, g);
-  set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+  set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
   a.vec_x = vec_ok(x);
   a.fast = a.vec_x && full_widths(p);
   a.stats_out = stats;
@@ -416,8 +416,6 @@ int32_t fs_compute_stats(const fs_points* x, const fs_slice_params* p, float* st
   int32_t rc = check_params(p, who);
   if (!rc) rc = check_points(x, "x_mid", p->D, who);
   if (rc) return rc;
-  if (p->row_splits)
-    return fail(FS_ERR_UNSUPPORTED, "%s: statistics are not supported with row splits", who);
   if (!stats) return fail(FS_ERR_INVALID, "%s: stats is NULL", who);
   const Workspace ws = plan_ws(FS_OP_STATS, p, (char*)workspace);
   rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
@@ -451,8 +449,6 @@ int32_t slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_params
   if (rc) return rc;
   if (fx->dtype != x->dtype) return fail(FS_ERR_INVALID, "%s: x_mid and fx_mid dtypes differ", who);
   if (!z_num || !s) return fail(FS_ERR_INVALID, "%s: z_num and s must be non-NULL", who);
-  rc = check_rows(p, stats_in, stats_out, who);
-  if (rc) return rc;
   const Workspace ws = plan_ws(FS_OP_SLICE_FWD, p, (char*)workspace);
   rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
   if (rc) return rc;
@@ -466,20 +462,19 @@ int32_t slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_params
     // handed-in statistics (of these very logits) are not needed
     g = geo_n(p, fused_target(FS_OP_SLICE_FWD, p));
     fs::Args a = base_args(p, g);
-    set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
-    set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
+    set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_in(p, fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
     a.vec_x = vec_ok(x);
     a.vec_f = vec_ok(fx);
     a.fast = a.vec_x && a.vec_f && full_widths(p);
     a.part = ws.part;
     a.stats_out = stats_out;
-    ragged_strides(a);
     rc = hip_check(fs::launch_fused_slice_fwd(a, x->dtype, mode, st), who);
   } else {
     g = geo_g(p, mode);
     fs::Args a = base_args(p, g);
-    set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
-    set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
+    set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_in(p, fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
     a.vec_x = vec_ok(x);
     a.vec_f = vec_ok(fx);
     a.fast = a.vec_x && a.vec_f && full_widths(p);
@@ -576,8 +571,6 @@ int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float
   if (rc) return rc;
   if (out->dtype != x->dtype) return fail(FS_ERR_INVALID, "%s: out and x_mid dtypes differ", who);
   if (!tokens) return fail(FS_ERR_INVALID, "%s: tokens is NULL", who);
-  rc = check_rows(p, stats_in, stats_out, who);
-  if (rc) return rc;
   const Workspace ws = plan_ws(FS_OP_DESLICE_FWD, p, (char*)workspace);
   rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
   if (rc) return rc;
@@ -586,20 +579,19 @@ int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float
   if (family_of(p) == 1) {
     const Geo g = geo_n(p, fused_target(FS_OP_DESLICE_FWD, p));
     fs::Args a = base_args(p, g);
-    set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
-    set_out(out, &a.o1, &a.s1b, &a.s1n, &a.s1h);
+    set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_out(p, out, &a.o1, &a.s1b, &a.s1n, &a.s1h);
     a.vec_x = vec_ok(x);
     a.vec_1 = vec_ok(out);
     a.fast = a.vec_x && a.vec_1 && full_widths(p);
     a.tok = tokens;
     a.stats_out = stats_out;
-    ragged_strides(a);
     return hip_check(fs::launch_fused_deslice_fwd(a, x->dtype, mode, st), who);
   }
   const Geo g = geo_gp(p, GPG_DESLICE, mode);
   fs::Args a = base_args(p, g);
-  set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
-  set_out(out, &a.o1, &a.s1b, &a.s1n, &a.s1h);
+  set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+  set_out(p, out, &a.o1, &a.s1b, &a.s1n, &a.s1h);
   a.vec_x = vec_ok(x);
   a.vec_1 = vec_ok(out);
   a.fast = a.vec_x && a.vec_1 && full_widths(p);
@@ -629,8 +621,6 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     return fail(FS_ERR_INVALID, "%s: point tensors must share one dtype", who);
   if (!dz_num || !ds || !dweight || !dbias || !dtau)
     return fail(FS_ERR_INVALID, "%s: dz_num, ds, dweight, dbias, dtau must be non-NULL", who);
-  rc = check_rows(p, stats_in, nullptr, who);
-  if (rc) return rc;
   const Workspace ws = plan_ws(FS_OP_SLICE_BWD, p, (char*)workspace);
   rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
   if (rc) return rc;
@@ -644,10 +634,10 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
   if (family_of(p) == 1) {
     const Geo g = geo_n(p, fused_target(FS_OP_SLICE_BWD, p));
     fs::Args a = base_args(p, g);
-    set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
-    set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
-    set_out(dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
-    set_out(dfx, &a.o2, &a.s2b, &a.s2n, &a.s2h);
+    set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_in(p, fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
+    set_out(p, dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
+    set_out(p, dfx, &a.o2, &a.s2b, &a.s2n, &a.s2h);
     a.vec_x = vec_ok(x);
     a.vec_f = vec_ok(fx);
     a.vec_1 = vec_ok(dx);
@@ -656,7 +646,6 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     a.tok = dz_num;
     a.ds = ds;
     a.part = ws.part;
-    ragged_strides(a);
     rc = hip_check(fs::launch_fused_slice_bwd(a, x->dtype, mode, st), who);
     if (rc) return rc;
     rs.seg[0] = seg(ws.part, wf, 0, pb(g), G * D, Bw, Hw, dweight);
@@ -665,10 +654,10 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
   } else {
     const Geo gn = geo_gp(p, GPG_BWD_N, mode), gg = geo_g(p, mode);
     fs::Args a = base_args(p, gn);
-    set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
-    set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
-    set_out(dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
-    set_out(dfx, &a.o2, &a.s2b, &a.s2n, &a.s2h);
+    set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_in(p, fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
+    set_out(p, dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
+    set_out(p, dfx, &a.o2, &a.s2b, &a.s2n, &a.s2h);
     a.vec_x = vec_ok(x);
     a.vec_f = vec_ok(fx);
     a.vec_1 = vec_ok(dx);
@@ -717,8 +706,6 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
   if (!tokens || !dtokens || !dweight || !dbias || !dtau)
     return fail(FS_ERR_INVALID, "%s: tokens, dtokens, dweight, dbias, dtau must be non-NULL",
                 who);
-  rc = check_rows(p, stats_in, nullptr, who);
-  if (rc) return rc;
   const Workspace ws = plan_ws(FS_OP_DESLICE_BWD, p, (char*)workspace);
   rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
   if (rc) return rc;
@@ -733,16 +720,15 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
   if (family_of(p) == 1) {
     const Geo g = geo_n(p, fused_target(FS_OP_DESLICE_BWD, p));
     fs::Args a = base_args(p, g);
-    set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
-    set_in(d_out, &a.f, &a.sfb, &a.sfn, &a.sfh);
-    set_out(dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
+    set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_in(p, d_out, &a.f, &a.sfb, &a.sfn, &a.sfh);
+    set_out(p, dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
     a.vec_x = vec_ok(x);
     a.vec_f = vec_ok(d_out);
     a.vec_1 = vec_ok(dx);
     a.fast = a.vec_x && a.vec_f && a.vec_1 && full_widths(p);
     a.tok = tokens;
     a.part = ws.part;
-    ragged_strides(a);
     rc = hip_check(fs::launch_fused_deslice_bwd(a, x->dtype, mode, st), who);
     if (rc) return rc;
     rs.seg[0] = seg(ws.part, wf, 0, pb(g), G * DV, (int)p->B, (int)p->H, dtokens);
@@ -753,9 +739,9 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
     const float* stats = stats_in;
     const Geo gn = geo_gp(p, GPG_BWD_N, mode), gg = geo_g(p, mode);
     fs::Args a = base_args(p, gn);
-    set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
-    set_in(d_out, &a.f, &a.sfb, &a.sfn, &a.sfh);
-    set_out(dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
+    set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_in(p, d_out, &a.f, &a.sfb, &a.sfn, &a.sfh);
+    set_out(p, dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
     a.vec_x = vec_ok(x);
     a.vec_f = vec_ok(d_out);
     a.vec_1 = vec_ok(dx);
@@ -812,8 +798,6 @@ int32_t fs_tied_bwd(const fs_points* x, const fs_points* fx, const fs_points* d_
     return fail(FS_ERR_UNSUPPORTED,
                 "%s: served by the whole-G kernels only (G <= 128 and D, DV small enough); "
                 "run fs_deslice_bwd and fs_slice_bwd", who);
-  rc = check_rows(p, nullptr, nullptr, who);
-  if (rc) return rc;
   const Workspace ws = plan_ws(FS_OP_TIED_BWD, p, (char*)workspace);
   rc = check_ws(ws.bytes, workspace_bytes, workspace, who);
   if (rc) return rc;
@@ -826,11 +810,11 @@ int32_t fs_tied_bwd(const fs_points* x, const fs_points* fx, const fs_points* d_
   const int Bb = Bo_of(p->b_stride_b, p->B), Hb = Ho_of(p->b_stride_h, p->H);
   const Geo g = geo_n(p, fused_target(FS_OP_TIED_BWD, p));
   fs::Args a = base_args(p, g);
-  set_in(x, &a.x, &a.sxb, &a.sxn, &a.sxh);
-  set_in(fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
-  set_in(d_out, &a.g, &a.sgb, &a.sgn, &a.sgh);
-  set_out(dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
-  if (want_dfx) set_out(dfx, &a.o2, &a.s2b, &a.s2n, &a.s2h);
+  set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+  set_in(p, fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
+  set_in(p, d_out, &a.g, &a.sgb, &a.sgn, &a.sgh);
+  set_out(p, dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
+  if (want_dfx) set_out(p, dfx, &a.o2, &a.s2b, &a.s2n, &a.s2h);
   a.vec_x = vec_ok(x);
   a.vec_f = vec_ok(fx) && vec_ok(d_out);
   a.vec_1 = vec_ok(dx);
@@ -840,7 +824,6 @@ int32_t fs_tied_bwd(const fs_points* x, const fs_points* fx, const fs_points* d_
   a.tok2 = tokens;
   a.ds = ds;
   a.part = ws.part;
-  ragged_strides(a);
   rc = hip_check(fs::launch_fused_tied_bwd(a, x->dtype, mode, st), who);
   if (rc) return rc;
   fs::ReduceSegments rs{};

@@ -112,17 +112,19 @@ __device__ __forceinline__ void load_rows_nb(float (&f)[NB][16], const T* base, 
 
 // saved statistics of point p (clamped to N - 1: finite for padded points,
 // whose results are masked): m in log2 units and l
-__device__ __forceinline__ void load_stats(float& m2, float& l, const float* stats, int bh, int N,
-                                           int p) {
-  const float* base = stats + (int64_t)bh * 2 * N;
+// (`sm`: this sample and head's max row, Rows::stats_off; its sum row NS
+// floats further)
+__device__ __forceinline__ void load_stats(float& m2, float& l, const float* sm, int64_t NS,
+                                           int N, int p) {
   const int q = p < N ? p : N - 1;
-  m2 = base[q] * kLog2e;
-  l = base[N + q];
+  m2 = sm[q] * kLog2e;
+  l = sm[NS + q];
 }
 
-// a per-point (B, H, N) fp32 value (clamped like load_stats)
-__device__ __forceinline__ float load_delta(const float* delta, int bh, int N, int p) {
-  return delta[(int64_t)bh * N + (p < N ? p : N - 1)];
+// a per-point fp32 value of this sample and head's row `row` (Rows::pt_off;
+// clamped like load_stats)
+__device__ __forceinline__ float load_delta(const float* row, int N, int p) {
+  return row[p < N ? p : N - 1];
 }
 
 #define BK_PROLOGUE                                                          \
@@ -131,7 +133,11 @@ __device__ __forceinline__ float load_delta(const float* delta, int bh, int N, i
   const int bh = blockIdx.y;                                                 \
   const int b = bh / a.H, hd = bh - b * a.H;                                \
   const int pid = blockIdx.x * kWavesPerBlock + wid;                         \
-  const int G = a.G, D = a.D, DV = a.DV, N = a.N, nd = a.nd, nv = a.nv;      \
+  const int G = a.G, D = a.D, DV = a.DV, nd = a.nd, nv = a.nv;               \
+  /* this sample's rows (row splits of a ragged batch) and per-point buffers */ \
+  const Rows R_ = rows_of(a, b, hd);                                         \
+  const int64_t row0_ = R_.row0;                                             \
+  const int N = R_.N, ntiles_ = R_.ntiles;                                   \
   const float* Wp = a.W + b * a.swb + hd * a.swh;                            \
   const float* Bp = a.bias + b * a.sbb + hd * a.sbh;                         \
   const float tauf = a.tau[hd];                                              \
@@ -139,15 +145,15 @@ __device__ __forceinline__ float load_delta(const float* delta, int bh, int N, i
   const float inv_tau = 1.f / tauf;                                          \
   const bool fast = a.fast != 0;                                             \
   const int ngt = (G + 31) / 32;                                             \
-  (void)inv_tau; (void)DV; (void)nv; (void)ngt; (void)fast;
+  (void)inv_tau; (void)DV; (void)nv; (void)ngt; (void)fast; (void)row0_;
 
 // ------------------------------------------------------------------ stats (n)
 template <typename T, int DK, int NB>
 __global__ __launch_bounds__(256, 2) void k_blk_stats(Args a) {
   constexpr int ML = Modes<DK>::L;
   BK_PROLOGUE
-  const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
-  for (int t = pid; t < a.ntiles; t += a.P) {
+  const T* xb = (const T*)a.x + b * a.sxb + row0_ * a.sxn + hd * a.sxh;
+  for (int t = pid; t < ntiles_; t += a.P) {
     const int p = t * kTile + c;
     const bool pv = p < N;
     float xf[NB][16];
@@ -197,7 +203,8 @@ __global__ __launch_bounds__(256, 2) void k_blk_stats(Args a) {
       l = l * __builtin_amdgcn_exp2f(m - mm) + lo * __builtin_amdgcn_exp2f(mo - mm);
       m = mm;
     }
-    store_stats(a.stats_out, bh, N, p, pv, h, m, l, a.two_pass != 0);
+    store_stats(a.stats_out ? a.stats_out + R_.stats_off() : nullptr, R_.NS, p, pv, h, m, l,
+                a.two_pass != 0);
   }
 }
 
@@ -211,10 +218,10 @@ __global__ __launch_bounds__(256, 2) void k_blk_deslice(Args a) {
   __shared__ float smem_rows[kWavesPerBlock * 32];
   BK_PROLOGUE
   float* lds_x = smem_rows + wid * 32;
-  const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
-  T* ob = (T*)a.o1 + b * a.s1b + hd * a.s1h;
+  const T* xb = (const T*)a.x + b * a.sxb + row0_ * a.sxn + hd * a.sxh;
+  T* ob = (T*)a.o1 + b * a.s1b + row0_ * a.s1n + hd * a.s1h;
   const float* Tp = a.tok + (int64_t)bh * G * DV;
-  for (int t = pid; t < a.ntiles; t += a.P) {
+  for (int t = pid; t < ntiles_; t += a.P) {
     const int p = t * kTile + c;
     const bool pv = p < N;
     float xf[NB][16];
@@ -223,7 +230,7 @@ __global__ __launch_bounds__(256, 2) void k_blk_deslice(Args a) {
     // exponentials it accumulates (formed here, lane-local then the partner),
     // so each row of weights sums to one to one summation's precision
     float m2 = -INFINITY, l = 0.f, lown = 0.f;
-    if (!ONLINE) load_stats(m2, l, a.stats_in, bh, N, p);
+    if (!ONLINE) load_stats(m2, l, a.stats_in + R_.stats_off(), R_.NS, N, p);
     f32x16 acc[NB];
 #pragma unroll
     for (int k = 0; k < NB; ++k) acc[k] = zero16();
@@ -282,7 +289,8 @@ __global__ __launch_bounds__(256, 2) void k_blk_deslice(Args a) {
         for (int r = 0; r < 16; ++r) o[r] *= inv_r[r];
         store_cols<T>(ob, a.s1n, o, t * kTile, N, 32 * k, DV, c, h);
       }
-    if (ONLINE) store_stats(a.stats_out, bh, N, p, pv, h, m2, l);
+    if (ONLINE)
+      store_stats(a.stats_out ? a.stats_out + R_.stats_off() : nullptr, R_.NS, p, pv, h, m2, l);
   }
 }
 
@@ -301,9 +309,9 @@ __global__ __launch_bounds__(256, 2) void k_blk_slice_g(Args a) {
   float sacc = 0.f;
 #pragma unroll
   for (int k = 0; k < NB; ++k) zacc[k] = zero16();
-  const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
-  const T* fb = (const T*)a.f + b * a.sfb + hd * a.sfh;
-  for (int t = pid, it = 0; t < a.ntiles; t += a.P, ++it) {
+  const T* xb = (const T*)a.x + b * a.sxb + row0_ * a.sxn + hd * a.sxh;
+  const T* fb = (const T*)a.f + b * a.sfb + row0_ * a.sfn + hd * a.sfh;
+  for (int t = pid, it = 0; t < ntiles_; t += a.P, ++it) {
     const int p0 = t * kTile, p = p0 + c;
     const bool pv = p < N;
     float xf[NB][16];
@@ -317,7 +325,7 @@ __global__ __launch_bounds__(256, 2) void k_blk_slice_g(Args a) {
         fT[k][j] = (k < nv && pj < N && v < DV) ? to_f<T>(fb[(int64_t)pj * a.sfn + v]) : 0.f;
       }
     float m2, l;
-    load_stats(m2, l, a.stats_in, bh, N, p);
+    load_stats(m2, l, a.stats_in + R_.stats_off(), R_.NS, N, p);
     float t2[16], w[16];
     blk_logits<ML, NB>(t2, wA, xf, bc, cst, nd);
     const float sg = tile_sign(it);  // the weights carry the tile's sign (acc_add)
@@ -364,21 +372,21 @@ __global__ __launch_bounds__(256, 2) void k_blk_bwd_n(Args a) {
   __shared__ float smem_rows[kWavesPerBlock * 32];
   BK_PROLOGUE
   float* lds_x = smem_rows + wid * 32;
-  const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
-  const T* fb = (const T*)a.f + b * a.sfb + hd * a.sfh;
-  T* dxb = (T*)a.o1 + b * a.s1b + hd * a.s1h;
-  T* dfb = SLICE ? (T*)a.o2 + b * a.s2b + hd * a.s2h : nullptr;
+  const T* xb = (const T*)a.x + b * a.sxb + row0_ * a.sxn + hd * a.sxh;
+  const T* fb = (const T*)a.f + b * a.sfb + row0_ * a.sfn + hd * a.sfh;
+  T* dxb = (T*)a.o1 + b * a.s1b + row0_ * a.s1n + hd * a.s1h;
+  T* dfb = SLICE ? (T*)a.o2 + b * a.s2b + row0_ * a.s2n + hd * a.s2h : nullptr;
   const float* Zp = a.tok + (int64_t)bh * G * DV;  // dz_num (slice) or tokens (deslice)
   const float* Sp = SLICE ? a.ds + (int64_t)bh * G : nullptr;
   float dtacc = 0.f;
-  for (int t = pid; t < a.ntiles; t += a.P) {
+  for (int t = pid; t < ntiles_; t += a.P) {
     const int p = t * kTile + c;
     const bool pv = p < N;
     float xf[NB][16], ff[NB][16];
     load_rows_nb<T, NB>(xf, xb, a.sxn, p, N, D, nd, fast, a.vec_x, h);
     load_rows_nb<T, NB>(ff, fb, a.sfn, p, N, DV, nv, fast, a.vec_f, h);
     float m2, lsaved;
-    load_stats(m2, lsaved, a.stats_in, bh, N, p);
+    load_stats(m2, lsaved, a.stats_in + R_.stats_off(), R_.NS, N, p);
     (void)lsaved;
     // pass 1: the row sum l is formed here from the same exponentials, so
     // sum_g dl vanishes to one summation's precision whatever rounding the
@@ -424,8 +432,8 @@ __global__ __launch_bounds__(256, 2) void k_blk_bwd_n(Args a) {
     const float inv_l = 1.f / l;
     const float delta = sdw * inv_l;
     if (pv && h == 0) {
-      a.delta[(int64_t)bh * N + p] = delta;
-      a.lsum[(int64_t)bh * N + p] = l;
+      a.delta[R_.pt_off() + p] = delta;
+      a.lsum[R_.pt_off() + p] = l;
     }
     if (SLICE) {
       // dfx is [v-outer, point-inner]: scale register r by its point's 1/l
@@ -517,18 +525,18 @@ __global__ __launch_bounds__(256, 2) void k_blk_bwd_g(Args a) {
     dW[k] = zero16();
     dT[k] = zero16();
   }
-  const T* xb = (const T*)a.x + b * a.sxb + hd * a.sxh;
-  const T* fb = (const T*)a.f + b * a.sfb + hd * a.sfh;
-  for (int t = pid, it = 0; t < a.ntiles; t += a.P, ++it) {
+  const T* xb = (const T*)a.x + b * a.sxb + row0_ * a.sxn + hd * a.sxh;
+  const T* fb = (const T*)a.f + b * a.sfb + row0_ * a.sfn + hd * a.sfh;
+  for (int t = pid, it = 0; t < ntiles_; t += a.P, ++it) {
     const int p = t * kTile + c;
     const bool pv = p < N;
     float xf[NB][16], ff[NB][16];
     load_rows_nb<T, NB>(xf, xb, a.sxn, p, N, D, nd, fast, a.vec_x, h);
     load_rows_nb<T, NB>(ff, fb, a.sfn, p, N, DV, nv, fast, a.vec_f, h);
     float m2, l;
-    load_stats(m2, l, a.stats_in, bh, N, p);
-    l = load_delta(a.lsum, bh, N, p);  // the row sum the point-owned pass formed
-    const float delta = load_delta(a.delta, bh, N, p);
+    load_stats(m2, l, a.stats_in + R_.stats_off(), R_.NS, N, p);
+    l = load_delta(a.lsum + R_.pt_off(), N, p);  // the row sum the point-owned pass formed
+    const float delta = load_delta(a.delta + R_.pt_off(), N, p);
     float t2[16], w[16];
     blk_logits<ML, NB>(t2, wA, xf, bc, cst, nd);
     // the weights -- and through them Lb -- carry the tile's sign (acc_add)

@@ -92,10 +92,7 @@ __device__ __forceinline__ void block_partial(float* buf, int E, int wid, float*
   __syncthreads();
 }
 __device__ __forceinline__ void acc_put(float& t, float v, bool first) { t = first ? v : t + v; }
-// a row split held to [lo, hi] (ragged batches: splits are read on the device only)
-__device__ __forceinline__ int64_t clamp_rows(int64_t v, int64_t lo, int64_t hi) {
-  return v < lo ? lo : (v > hi ? hi : v);
-}
+
 
 // Block prologue shared by the four kernels: head constants, LDS carve-up,
 // the fp32 staging of W and tokens / dz_num, and the logits operand W
@@ -112,13 +109,12 @@ __device__ __forceinline__ int64_t clamp_rows(int64_t v, int64_t lo, int64_t hi)
   const int bh = blockIdx.y;                                                        \
   const int b = bh / a.H, hd = bh - b * a.H;                                       \
   const int pid = blockIdx.x * kWavesPerBlock + wid;                                \
-  /* row splits (ragged batch): sample b is rows rows[b] .. rows[b + 1] - 1,      \
-     clamped to the point tensors' rows and to N rows per sample */                 \
-  const int64_t row0_ = a.rows ? clamp_rows(a.rows[b], 0, a.rows_total) : 0;        \
+  /* this sample's rows (row splits of a ragged batch) and per-point buffers */   \
+  const Rows R_ = rows_of(a, b, hd);                                                \
+  const int64_t row0_ = R_.row0;                                                    \
   const int G = a.G, D = a.D, DV = a.DV;                                            \
-  const int N = a.rows ? (int)min(clamp_rows(a.rows[b + 1], row0_, a.rows_total) - row0_, \
-                                  (int64_t)a.N) : a.N;                              \
-  const int ntiles_ = a.rows ? (N + kTile - 1) / kTile : a.ntiles;                  \
+  const int N = R_.N;                                                               \
+  const int ntiles_ = R_.ntiles;                                                    \
   float* sW = smem;                                                                 \
   float* sV = smem + SM::GP * SM::SW;                                               \
   float* lds = smem + wid * (WF);                                                   \
@@ -199,8 +195,8 @@ __global__ __launch_bounds__(256, NGB * NDB * NVB == 1 ? 3 : 1) void k_fused_sli
   uint32_t vcf[NVB];  // fx is read as [v-outer, point-inner]: whole-row loads
 #pragma unroll
   for (int vb = 0; vb < NVB; ++vb) vcf[vb] = col_off<T>(vb, DV, f_sn, c, h);
-  const float* st_m = a.stats_out ? a.stats_out + (int64_t)bh * 2 * N : nullptr;
-  const float* st_l = st_m ? st_m + N : nullptr;
+  const float* st_m = a.stats_out ? a.stats_out + R_.stats_off() : nullptr;
+  const float* st_l = st_m ? st_m + R_.NS : nullptr;
   auto run = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
     const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
@@ -365,8 +361,8 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
   uint32_t vco[NVB];  // out is written as [v-outer, point-inner]: whole-row stores
 #pragma unroll
   for (int vb = 0; vb < NVB; ++vb) vco[vb] = col_off<T>(vb, DV, o_sn, c, h);
-  const float* st_m = a.stats_out ? a.stats_out + (int64_t)bh * 2 * N : nullptr;
-  const float* st_l = st_m ? st_m + N : nullptr;
+  const float* st_m = a.stats_out ? a.stats_out + R_.stats_off() : nullptr;
+  const float* st_l = st_m ? st_m + R_.NS : nullptr;
   auto run = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
     const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;

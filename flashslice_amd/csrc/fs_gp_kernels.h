@@ -154,10 +154,9 @@ __device__ __forceinline__ void gp_vec(float (&v)[16], const u32x4* item, int la
   const int lane = threadIdx.x & 63;                                              \
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);               \
   const int c = lane & 31, h = lane >> 5;                                         \
-  const int G = a.G, D = a.D, DV = a.DV, N = a.N, nd = a.nd, nv = a.nv;           \
-  const int ntiles_ = a.ntiles;                                                   \
+  const int G = a.G, D = a.D, DV = a.DV, nd = a.nd, nv = a.nv;                    \
   const int ngb = (G + 31) / 32;                                                  \
-  (void)D; (void)DV; (void)nd; (void)nv; (void)ntiles_;
+  (void)D; (void)DV; (void)nd; (void)nv;
 
 #define GP_HEAD(BH)                                                               \
   const int bh = (BH);                                                            \
@@ -167,11 +166,16 @@ __device__ __forceinline__ void gp_vec(float (&v)[16], const u32x4* item, int la
   const float inv_tau = 1.f / tauf;                                               \
   const bool fast = a.fast != 0;                                                  \
   const u32x4* fr = reinterpret_cast<const u32x4*>(a.frags);                     \
-  (void)inv_tau; (void)fast; (void)b;
+  /* this sample's rows (row splits of a ragged batch) and per-point buffers */ \
+  const Rows R_ = rows_of(a, b, hd);                                              \
+  const int64_t row0_ = R_.row0;                                                  \
+  const int N = R_.N, ntiles_ = R_.ntiles;                                        \
+  (void)inv_tau; (void)fast; (void)b; (void)row0_; (void)ntiles_;
 
 // point slice of one (b, h): byte base, row stride, row width, lane row
 #define GP_SLICE(NAME, PTR, SB, SN, SH, C)                                                \
-  const char* NAME##_b = (const char*)(PTR) + (b * (SB) + hd * (SH)) * (int64_t)sizeof(T); \
+  const char* NAME##_b =                                                                  \
+      (const char*)(PTR) + (b * (SB) + row0_ * (SN) + hd * (SH)) * (int64_t)sizeof(T);    \
   const int64_t NAME##_sn = (SN) * (int64_t)sizeof(T);                                    \
   const int64_t NAME##_w = (int64_t)(C) * (int64_t)sizeof(T);                             \
   const uint32_t NAME##_row = (uint32_t)(c * NAME##_sn);
@@ -220,8 +224,8 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_stats(Args a) {
   GP_PROLOGUE
   GP_HEAD(blockIdx.y)
   GP_SLICE(x, a.x, a.sxb, a.sxn, a.sxh, D)
-  const float* sm = a.stats_out ? a.stats_out + (int64_t)bh * 2 * N : nullptr;
-  const float* sl = sm ? sm + N : nullptr;
+  const float* sm = a.stats_out ? a.stats_out + R_.stats_off() : nullptr;
+  const float* sl = sm ? sm + R_.NS : nullptr;
   const int passes = a.two_pass ? 2 : 1, nstage = passes * ngb;
   auto stage = [&](int buf, int s) {
     const int gb = s % ngb;
@@ -233,9 +237,9 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_stats(Args a) {
   __syncthreads();
   for (int it = 0;; ++it) {
     const int tb = kWavesPerBlock * (blockIdx.x + it * gridDim.x);
-    if (tb >= a.ntiles) break;
+    if (tb >= ntiles_) break;
     const int64_t p0 = (int64_t)(tb + wid) * kTile;
-    const bool more = tb + kWavesPerBlock * (int)gridDim.x < a.ntiles;
+    const bool more = tb + kWavesPerBlock * (int)gridDim.x < ntiles_;
     float xf[NB][16];
     gp_rows<T, NB>(xf, rows_rsrc(x_b, x_sn, x_w, p0, N), x_row, fast, D, h);
     Frag<ML> xq[NB];
@@ -306,10 +310,10 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_deslice(Args a) {
   uint32_t vco[NB];
 #pragma unroll
   for (int k = 0; k < NB; ++k) vco[k] = col_off<T>(k, DV, o_sn, c, h);
-  const float* sin_m = ONLINE ? nullptr : a.stats_in + (int64_t)bh * 2 * N;
+  const float* sin_m = ONLINE ? nullptr : a.stats_in + R_.stats_off();
   // the statistics are optional output of the online pass (null: not kept)
-  const float* sout_m = (ONLINE && a.stats_out) ? a.stats_out + (int64_t)bh * 2 * N : nullptr;
-  const float* sout_l = sout_m ? sout_m + N : nullptr;
+  const float* sout_m = (ONLINE && a.stats_out) ? a.stats_out + R_.stats_off() : nullptr;
+  const float* sout_l = sout_m ? sout_m + R_.NS : nullptr;
   auto stage = [&](int buf, int gb) {
     gp_stage(sbuf[buf], GP_ITEM(GP_WR, nd, gb, FWL), nd * Frag<ML>::W, wid, lane);
     gp_stage(sbuf[buf] + NB * FWL, GP_ITEM(GP_VC, nv, gb, FWV), nv * Frag<MV>::W, wid, lane);
@@ -320,10 +324,10 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_deslice(Args a) {
   __syncthreads();
   for (int it = 0;; ++it) {
     const int tb = kWavesPerBlock * (blockIdx.x + it * gridDim.x);
-    if (tb >= a.ntiles) break;
+    if (tb >= ntiles_) break;
     const int64_t p0 = (int64_t)(tb + wid) * kTile;
     const bool pv = p0 + c < N;
-    const bool more = tb + kWavesPerBlock * (int)gridDim.x < a.ntiles;
+    const bool more = tb + kWavesPerBlock * (int)gridDim.x < ntiles_;
     float xf[NB][16];
     gp_rows<T, NB>(xf, rows_rsrc(x_b, x_sn, x_w, p0, N), x_row, fast, D, h);
     Frag<ML> xq[NB];
@@ -425,7 +429,7 @@ __global__ __launch_bounds__(256, NB == 1 ? 3 : 1) void k_gp_slice_g(Args a) {
   uint32_t vcf[NB];
 #pragma unroll
   for (int k = 0; k < NB; ++k) vcf[k] = col_off<T>(k, DV, f_sn, c, h);
-  const float* sm = a.stats_in + (int64_t)bh * 2 * N;
+  const float* sm = a.stats_in + R_.stats_off();
   auto run = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
     const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
@@ -441,7 +445,7 @@ __global__ __launch_bounds__(256, NB == 1 ? 3 : 1) void k_gp_slice_g(Args a) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
       const float m2 = ld_pt(pts_rsrc(sm, p0, N), c) * kLog2e;
-      const float l = ld_pt(pts_rsrc(sm + N, p0, N), c);
+      const float l = ld_pt(pts_rsrc(sm + R_.NS, p0, N), c);
       Frag<ML> xq[NB];
 #pragma unroll
       for (int k = 0; k < NB; ++k) prep<ML>(xq[k], xf[k]);
@@ -522,9 +526,9 @@ __global__ __launch_bounds__(256, NB == 1 ? 3 : gp_waves(NB)) void k_gp_bwd_n(Ar
     vcx[k] = col_off<T>(k, D, dx_sn, c, h);
     vcf[k] = col_off<T>(k, DV, df_sn, c, h);
   }
-  const float* sm = a.stats_in + (int64_t)bh * 2 * N;
-  const float* sdel = a.delta + (int64_t)bh * N;
-  const float* slsum = a.lsum + (int64_t)bh * N;
+  const float* sm = a.stats_in + R_.stats_off();
+  const float* sdel = a.delta + R_.pt_off();
+  const float* slsum = a.lsum + R_.pt_off();
   const int nstage = 2 * ngb;
   auto stage = [&](int buf, int s) {
     const int gb = s % ngb, pass = s / ngb;
@@ -544,10 +548,10 @@ __global__ __launch_bounds__(256, NB == 1 ? 3 : gp_waves(NB)) void k_gp_bwd_n(Ar
   __syncthreads();
   for (int it = 0;; ++it) {
     const int tb = kWavesPerBlock * (blockIdx.x + it * gridDim.x);
-    if (tb >= a.ntiles) break;
+    if (tb >= ntiles_) break;
     const int64_t p0 = (int64_t)(tb + wid) * kTile;
     const bool pv = p0 + c < N;
-    const bool more = tb + kWavesPerBlock * (int)gridDim.x < a.ntiles;
+    const bool more = tb + kWavesPerBlock * (int)gridDim.x < ntiles_;
     float xf[NB][16], ff[NB][16];
     gp_rows<T, NB>(xf, rows_rsrc(x_b, x_sn, x_w, p0, N), x_row, fast, D, h);
     gp_rows<T, NB>(ff, rows_rsrc(f_b, f_sn, f_w, p0, N), f_row, fast, DV, h);
@@ -714,9 +718,9 @@ __global__ __launch_bounds__(256, NB == 1 && SLICE ? 3 : gp_waves(NB)) void k_gp
   }
   GP_SLICE(x, a.x, a.sxb, a.sxn, a.sxh, D)
   GP_SLICE(f, a.f, a.sfb, a.sfn, a.sfh, DV)
-  const float* sm = a.stats_in + (int64_t)bh * 2 * N;
-  const float* sdel = a.delta + (int64_t)bh * N;
-  const float* slsum = a.lsum + (int64_t)bh * N;
+  const float* sm = a.stats_in + R_.stats_off();
+  const float* sdel = a.delta + R_.pt_off();
+  const float* slsum = a.lsum + R_.pt_off();
   auto run = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
     const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;

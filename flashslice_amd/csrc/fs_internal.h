@@ -32,7 +32,7 @@ struct Args {
   float* part;                             // per-wave partials (workspace)
   float* part2;                            // per-wave dtau partials of point-owned kernels
   const int64_t* rows;                     // row splits (B + 1) of a ragged batch, or null
-                                           // (whole-G family; point strides along b are 0)
+                                           // (point strides along b are then 0; rows_of)
   int64_t rows_total;                      // rows of the ragged batch's point tensors
   int B, N, H, D, DV, G;
   int P;                                   // point partitions per (b, h), a multiple of 4
@@ -47,6 +47,43 @@ struct Args {
   void* frags;
   int64_t foff[6];
 };
+
+// The row range of sample b and where its per-point buffers start. Without
+// row splits: the sample's N points from row 0 of its slice of every point
+// tensor, and per-point buffers -- statistics (planes, 2, NS), delta and
+// row sums (planes, NS) -- in plane b * H + h of NS = N rows. With row
+// splits (a ragged batch): rows rows[b] .. rows[b + 1] - 1 of the
+// concatenated point tensors (clamped to their rows_total rows and to N rows
+// per sample, so malformed splits cannot address outside the tensors), and
+// per-point buffers in plane h of NS = rows_total rows, indexed by row: the
+// statistics of a ragged batch are (1, H, 2, rows_total).
+struct Rows {
+  int64_t row0, plane, NS;
+  int N, ntiles;
+  __device__ int64_t stats_off() const { return plane * 2 * NS + row0; }
+  __device__ int64_t pt_off() const { return plane * NS + row0; }
+};
+__device__ __forceinline__ int64_t clamp_rows(int64_t v, int64_t lo, int64_t hi) {
+  return v < lo ? lo : (v > hi ? hi : v);
+}
+__device__ __forceinline__ Rows rows_of(const Args& a, int b, int hd) {
+  Rows r;
+  if (!a.rows) {
+    r.row0 = 0;
+    r.plane = (int64_t)b * a.H + hd;
+    r.NS = a.N;
+    r.N = a.N;
+    r.ntiles = a.ntiles;
+    return r;
+  }
+  r.row0 = clamp_rows(a.rows[b], 0, a.rows_total);
+  const int64_t r1 = clamp_rows(a.rows[b + 1], r.row0, a.rows_total);
+  r.N = (int)(r1 - r.row0 < (int64_t)a.N ? r1 - r.row0 : (int64_t)a.N);
+  r.ntiles = (r.N + 31) / 32;
+  r.plane = hd;
+  r.NS = a.rows_total;
+  return r;
+}
 
 // Kinds of prepared fragments (G-blocked family): W [g-outer, d-inner] in the
 // logits mode; W / tau [d-outer, g-inner], V [g-outer, v-inner] and V

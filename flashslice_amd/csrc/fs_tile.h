@@ -80,15 +80,15 @@ __device__ __forceinline__ float stats_max_roundtrip(float m2) { return (m2 * kL
 // Softmax statistics of one point in the reference layout (B, H, 2, N):
 // the row max of the natural-unit logits and the sum of exponentials
 // against the max consumers will read back (reference blocked.py:1329-1335).
-// `l` is the sum against `m2`; it is rescaled once to the round-tripped max.
-// Written by lane h = 0 of each pair.
+// `sm` is this sample and head's max row (Rows::stats_off), its sum row NS
+// floats further. `l` is the sum against `m2`; it is rescaled once to the
+// round-tripped max. Written by lane h = 0 of each pair.
 // `l_roundtrip`: l is already the sum against stats_max_roundtrip(m2).
-__device__ __forceinline__ void store_stats(float* stats, int bh, int N, int p, bool pv, int h,
+__device__ __forceinline__ void store_stats(float* sm, int64_t NS, int p, bool pv, int h,
                                             float m2, float l, bool l_roundtrip = false) {
-  if (stats && pv && h == 0) {
-    float* base = stats + (int64_t)bh * 2 * N;
-    base[p] = m2 * kLn2;
-    base[N + p] = l_roundtrip ? l : l * __builtin_amdgcn_exp2f(m2 - stats_max_roundtrip(m2));
+  if (sm && pv && h == 0) {
+    sm[p] = m2 * kLn2;
+    sm[NS + p] = l_roundtrip ? l : l * __builtin_amdgcn_exp2f(m2 - stats_max_roundtrip(m2));
   }
 }
 

@@ -359,6 +359,9 @@ def _hip_slice_fwd(x_mid, fx_mid, weight, bias, tau, dot, stats_in=None, want_st
                    rows=None):
     B, N, H, D = x_mid.shape
     DV = fx_mid.shape[3]
+    # statistics: (B, H, 2, N), or (1, H, 2, rows) for a ragged batch's
+    # (1, rows, H, D) view of its points
+    sshape = (B, H, 2, N)
     with torch.cuda.device(x_mid.device):
         call = _Call(x_mid, weight, bias, tau, DV, dot, rows)
         B = call.B
@@ -367,8 +370,8 @@ def _hip_slice_fwd(x_mid, fx_mid, weight, bias, tau, dot, stats_in=None, want_st
         x, fx = _as_points(x_mid, dt), _as_points(fx_mid, dt)
         z_num = torch.empty(B, H, call.G, DV, device=x.device, dtype=torch.float32)
         s = torch.empty(B, H, call.G, device=x.device, dtype=torch.float32)
-        st_in = None if stats_in is None else _small(stats_in, (B, H, 2, N), "stats", x.device)
-        st_out = (torch.empty(B, H, 2, N, device=x.device, dtype=torch.float32)
+        st_in = None if stats_in is None else _small(stats_in, sshape, "stats", x.device)
+        st_out = (torch.empty(sshape, device=x.device, dtype=torch.float32)
                   if want_stats and st_in is None else None)
         ws, nws = call.workspace(_hip.OP_SLICE_FWD)
         _hip.check(_hip.lib().fs_slice_fwd(

@@ -8,18 +8,22 @@ axis -- x_mid (rows, H, D), fx_mid (rows, H, DV) -- and ``row_splits``
 (B + 1 non-decreasing offsets, first 0, last = rows) says which rows are
 sample b's. Every sample gets its own slice sums (z_num, s of shape
 (B, H, G, DV), (B, H, G)); the slice projection may be shared (G, D),
-per head (H, G, D) or per sample (B, H, G, D), as in ``fused_slice``. The
-kernels are the whole-G family's: each (sample, head) block reads its row
-range from the splits, so no sample is padded and one launch covers all.
+per head (H, G, D) or per sample (B, H, G, D), as in ``fused_slice``. Each
+(sample, head) block of every kernel reads its row range from the splits,
+so no sample is padded and one launch covers all.
 
 ``row_splits`` on the CPU (a list or an int64 tensor) is validated and
 copied to the device; a device tensor is used as is, with ``max_rows`` (the
-longest sample, which sizes the launch) required and the splits trusted --
-the caller's contract, as reading them back would synchronise.
+longest sample, which sizes the launch) required and the splits not read
+back (that would synchronise): the kernels clamp them to the point tensors'
+rows, so malformed splits give wrong sums but stay in bounds.
 
-Shapes the whole-G kernels do not serve (G > 128, wide D / DV) and the
-softmax statistics are not supported with row splits (the library returns
-FS_ERR_UNSUPPORTED); kernel mode "blocked" refuses them too.
+Every shape the plain ops serve is served here, on both kernel families:
+the whole-G kernels where the slot axis fits in registers, the G-blocked
+ones (any G, widths up to 256) otherwise. The softmax statistics of a
+ragged batch are (1, H, 2, rows) fp32, indexed by row like the points;
+``return_stats`` / ``stats`` hand them from one op to the other as
+``fused_slice`` / ``fused_deslice`` do.
 """
 
 import torch
@@ -31,17 +35,17 @@ from .slice_ops import (
 
 _LIB.define(
     "slice_varlen(Tensor x_mid, Tensor fx_mid, Tensor weight, Tensor bias, Tensor tau, "
-    "Tensor row_splits, int max_rows, int dot) -> (Tensor, Tensor)")
+    "Tensor row_splits, int max_rows, Tensor? stats, int dot) -> (Tensor, Tensor, Tensor)")
 _LIB.define(
     "slice_varlen_bwd(Tensor x_mid, Tensor fx_mid, Tensor weight, Tensor bias, Tensor tau, "
-    "Tensor row_splits, int max_rows, Tensor dz_num, Tensor ds, int dot) "
+    "Tensor row_splits, int max_rows, Tensor stats, Tensor dz_num, Tensor ds, int dot) "
     "-> (Tensor, Tensor, Tensor, Tensor, Tensor)")
 _LIB.define(
     "deslice_varlen(Tensor x_mid, Tensor weight, Tensor bias, Tensor tau, Tensor tokens, "
-    "Tensor row_splits, int max_rows, int dot) -> Tensor")
+    "Tensor row_splits, int max_rows, Tensor? stats, int dot) -> (Tensor, Tensor)")
 _LIB.define(
     "deslice_varlen_bwd(Tensor x_mid, Tensor weight, Tensor bias, Tensor tau, Tensor tokens, "
-    "Tensor row_splits, int max_rows, Tensor d_out, int dot) "
+    "Tensor row_splits, int max_rows, Tensor stats, Tensor d_out, int dot) "
     "-> (Tensor, Tensor, Tensor, Tensor, Tensor)")
 
 
@@ -54,28 +58,30 @@ def _pts(t):
     return t.unsqueeze(0)
 
 
-def _slice_varlen_impl(x_mid, fx_mid, weight, bias, tau, row_splits, max_rows, dot):
-    z_num, s, _ = _hip_slice_fwd(_pts(x_mid), _pts(fx_mid), weight, bias, tau, dot,
-                                 rows=_rows(row_splits, max_rows))
-    return z_num, s
+def _slice_varlen_impl(x_mid, fx_mid, weight, bias, tau, row_splits, max_rows, stats, dot):
+    return _hip_slice_fwd(_pts(x_mid), _pts(fx_mid), weight, bias, tau, dot, stats_in=stats,
+                          want_stats=True, rows=_rows(row_splits, max_rows))
 
 
-def _slice_varlen_bwd_impl(x_mid, fx_mid, weight, bias, tau, row_splits, max_rows, dz_num, ds,
-                           dot):
+def _slice_varlen_bwd_impl(x_mid, fx_mid, weight, bias, tau, row_splits, max_rows, stats, dz_num,
+                           ds, dot):
     dx, dfx, dw, db, dtau = _hip_slice_bwd(_pts(x_mid), _pts(fx_mid), weight, bias, tau, dz_num,
-                                           ds, dot, rows=_rows(row_splits, max_rows))
+                                           ds, dot, stats_in=stats,
+                                           rows=_rows(row_splits, max_rows))
     return dx[0], dfx[0], dw, db, dtau
 
 
-def _deslice_varlen_impl(x_mid, weight, bias, tau, tokens, row_splits, max_rows, dot):
-    out, _ = _hip_deslice_fwd(_pts(x_mid), weight, bias, tau, tokens, dot,
-                              rows=_rows(row_splits, max_rows))
-    return out[0]
+def _deslice_varlen_impl(x_mid, weight, bias, tau, tokens, row_splits, max_rows, stats, dot):
+    out, st = _hip_deslice_fwd(_pts(x_mid), weight, bias, tau, tokens, dot, stats_in=stats,
+                               want_stats=True, rows=_rows(row_splits, max_rows))
+    return out[0], st
 
 
-def _deslice_varlen_bwd_impl(x_mid, weight, bias, tau, tokens, row_splits, max_rows, d_out, dot):
+def _deslice_varlen_bwd_impl(x_mid, weight, bias, tau, tokens, row_splits, max_rows, stats, d_out,
+                             dot):
     dx, dtok, dw, db, dtau = _hip_deslice_bwd(_pts(x_mid), weight, bias, tau, tokens,
-                                              _pts(d_out), dot, rows=_rows(row_splits, max_rows))
+                                              _pts(d_out), dot, stats_in=stats,
+                                              rows=_rows(row_splits, max_rows))
     return dx[0], dtok, dw, db, dtau
 
 
@@ -85,59 +91,66 @@ _LIB.impl("deslice_varlen", _deslice_varlen_impl, "CUDA")
 _LIB.impl("deslice_varlen_bwd", _deslice_varlen_bwd_impl, "CUDA")
 
 
+def _stats_fake(x_mid):
+    return x_mid.new_empty((1, x_mid.shape[1], 2, x_mid.shape[0]), dtype=torch.float32)
+
+
 @torch.library.register_fake("flashslice::slice_varlen")
-def _(x_mid, fx_mid, weight, bias, tau, row_splits, max_rows, dot):
+def _(x_mid, fx_mid, weight, bias, tau, row_splits, max_rows, stats, dot):
     B, H, G = row_splits.shape[0] - 1, x_mid.shape[1], weight.shape[-2]
     return (x_mid.new_empty((B, H, G, fx_mid.shape[2]), dtype=torch.float32),
-            x_mid.new_empty((B, H, G), dtype=torch.float32))
+            x_mid.new_empty((B, H, G), dtype=torch.float32), _stats_fake(x_mid))
 
 
 @torch.library.register_fake("flashslice::slice_varlen_bwd")
-def _(x_mid, fx_mid, weight, bias, tau, row_splits, max_rows, dz_num, ds, dot):
+def _(x_mid, fx_mid, weight, bias, tau, row_splits, max_rows, stats, dz_num, ds, dot):
     return (torch.empty_like(x_mid), torch.empty_like(fx_mid), torch.empty_like(weight),
             torch.empty_like(bias), torch.empty_like(tau))
 
 
 @torch.library.register_fake("flashslice::deslice_varlen")
-def _(x_mid, weight, bias, tau, tokens, row_splits, max_rows, dot):
-    return x_mid.new_empty((x_mid.shape[0], x_mid.shape[1], tokens.shape[3]))
+def _(x_mid, weight, bias, tau, tokens, row_splits, max_rows, stats, dot):
+    return (x_mid.new_empty((x_mid.shape[0], x_mid.shape[1], tokens.shape[3])),
+            _stats_fake(x_mid))
 
 
 @torch.library.register_fake("flashslice::deslice_varlen_bwd")
-def _(x_mid, weight, bias, tau, tokens, row_splits, max_rows, d_out, dot):
+def _(x_mid, weight, bias, tau, tokens, row_splits, max_rows, stats, d_out, dot):
     return (torch.empty_like(x_mid), torch.empty_like(tokens), torch.empty_like(weight),
             torch.empty_like(bias), torch.empty_like(tau))
 
 
 def _slice_setup(ctx, inputs, output):
-    x_mid, fx_mid, weight, bias, tau, row_splits, max_rows, dot = inputs
-    ctx.save_for_backward(x_mid, fx_mid, weight, bias, tau, row_splits)
+    x_mid, fx_mid, weight, bias, tau, row_splits, max_rows, stats, dot = inputs
+    ctx.save_for_backward(x_mid, fx_mid, weight, bias, tau, row_splits, output[2])
     ctx.max_rows, ctx.dot = max_rows, dot
 
 
-def _slice_grad(ctx, dz_num, ds):
-    x_mid, fx_mid, weight, bias, tau, row_splits = ctx.saved_tensors
+def _slice_grad(ctx, dz_num, ds, dstats):
+    """The statistics are saved intermediates: an incoming gradient on them
+    is ignored (as the blocked ops', reference blocked.py:1538-1550)."""
+    x_mid, fx_mid, weight, bias, tau, row_splits, stats = ctx.saved_tensors
     B, H, G, DV = row_splits.shape[0] - 1, x_mid.shape[1], weight.shape[-2], fx_mid.shape[2]
     if dz_num is None:
         dz_num = torch.zeros(B, H, G, DV, device=x_mid.device, dtype=torch.float32)
     if ds is None:
         ds = torch.zeros(B, H, G, device=x_mid.device, dtype=torch.float32)
     dxm, dfx, dw, db, dtau = torch.ops.flashslice.slice_varlen_bwd(
-        x_mid, fx_mid, weight, bias, tau, row_splits, ctx.max_rows, dz_num, ds, ctx.dot)
-    return dxm, dfx, dw, db, dtau, None, None, None
+        x_mid, fx_mid, weight, bias, tau, row_splits, ctx.max_rows, stats, dz_num, ds, ctx.dot)
+    return dxm, dfx, dw, db, dtau, None, None, None, None
 
 
 def _deslice_setup(ctx, inputs, output):
-    x_mid, weight, bias, tau, tokens, row_splits, max_rows, dot = inputs
-    ctx.save_for_backward(x_mid, weight, bias, tau, tokens, row_splits)
+    x_mid, weight, bias, tau, tokens, row_splits, max_rows, stats, dot = inputs
+    ctx.save_for_backward(x_mid, weight, bias, tau, tokens, row_splits, output[1])
     ctx.max_rows, ctx.dot = max_rows, dot
 
 
-def _deslice_grad(ctx, d_out):
-    x_mid, weight, bias, tau, tokens, row_splits = ctx.saved_tensors
+def _deslice_grad(ctx, d_out, dstats):
+    x_mid, weight, bias, tau, tokens, row_splits, stats = ctx.saved_tensors
     dxm, dtok, dw, db, dtau = torch.ops.flashslice.deslice_varlen_bwd(
-        x_mid, weight, bias, tau, tokens, row_splits, ctx.max_rows, d_out, ctx.dot)
-    return dxm, dw, db, dtau, dtok, None, None, None
+        x_mid, weight, bias, tau, tokens, row_splits, ctx.max_rows, stats, d_out, ctx.dot)
+    return dxm, dw, db, dtau, dtok, None, None, None, None
 
 
 torch.library.register_autograd("flashslice::slice_varlen", _slice_grad,
@@ -180,32 +193,39 @@ def _prep(x_mid, weight, bias, row_splits, max_rows, dv):
     return weight, bias, rs, longest
 
 
-def fused_slice_varlen(x_mid, fx_mid, weight, bias, tau, row_splits, max_rows=None):
+def fused_slice_varlen(x_mid, fx_mid, weight, bias, tau, row_splits, max_rows=None,
+                       return_stats=False, stats=None):
     """Slice of a ragged batch: x_mid (rows, H, D), fx_mid (rows, H, DV),
     sample b = rows row_splits[b] .. row_splits[b+1]-1; weight (G, D),
     (H, G, D) or (B, H, G, D); bias None, (G,), (H, G) or (B, H, G); tau
     (H,). Returns fp32 z_num (B, H, G, DV) and s (B, H, G), each sample's
     equal to ``fused_slice`` on that sample alone (an empty sample gives
-    zeros)."""
+    zeros). ``stats`` (1, H, 2, rows): statistics of these very logits from
+    a tied ``fused_deslice_varlen(..., return_stats=True)``; with
+    ``return_stats=True`` the statistics are returned third (detached)."""
     weight, bias, rs, longest = _prep(x_mid, weight, bias, row_splits, max_rows,
                                       fx_mid.shape[2])
     if fx_mid.dim() != 3 or fx_mid.shape[:2] != x_mid.shape[:2]:
         raise ValueError("fx_mid must be (rows, H, DV) with x_mid's rows and heads")
-    return torch.ops.flashslice.slice_varlen(x_mid, fx_mid, weight, bias, tau, rs, longest,
-                                             _dot_mode(x_mid))
+    z_num, s, st = torch.ops.flashslice.slice_varlen(x_mid, fx_mid, weight, bias, tau, rs,
+                                                     longest, stats, _dot_mode(x_mid))
+    return (z_num, s, st.detach()) if return_stats else (z_num, s)
 
 
-def fused_deslice_varlen(x_mid, weight, bias, tau, tokens, row_splits, max_rows=None):
+def fused_deslice_varlen(x_mid, weight, bias, tau, tokens, row_splits, max_rows=None,
+                         stats=None, return_stats=False):
     """Deslice of a ragged batch: tokens (B, H, G, DV) per sample; returns out
     (rows, H, DV) in x_mid's dtype, each sample's rows equal to
-    ``fused_deslice`` on that sample alone."""
+    ``fused_deslice`` on that sample alone; ``stats`` / ``return_stats`` as
+    in ``fused_slice_varlen``."""
     weight, bias, rs, longest = _prep(x_mid, weight, bias, row_splits, max_rows,
                                       tokens.shape[3])
     if tokens.dim() != 4 or tokens.shape[0] != rs.shape[0] - 1:
         raise ValueError("tokens must be (B, H, G, DV) with B = %d samples, got shape %s"
                          % (rs.shape[0] - 1, tuple(tokens.shape)))
-    return torch.ops.flashslice.deslice_varlen(x_mid, weight, bias, tau, tokens, rs, longest,
-                                               _dot_mode(x_mid))
+    out, st = torch.ops.flashslice.deslice_varlen(x_mid, weight, bias, tau, tokens, rs, longest,
+                                                  stats, _dot_mode(x_mid))
+    return (out, st.detach()) if return_stats else out
 
 
 __all__ = ["fused_slice_varlen", "fused_deslice_varlen"]

@@ -8,8 +8,9 @@ tokens back onto the points, project out (``to_out``).
 
 ``use_fused_slice=True`` runs slice and deslice through the HIP operators of
 ``flashslice_amd.kernels``: x_mid and fx_mid go to the kernels as (B, N, H, D)
-views of the Linear outputs (no permuted copies), the deslice reuses the
-slice's softmax statistics when it shares the slice's projection, and the
+views of the Linear outputs (no permuted copies); when the deslice shares
+the slice's projection the two run as one ``fused_coupling``, whose
+backward is one merged pass over the points; the
 (B, H, N, G) membership tensor is never formed -- on the eager route it is
 formed and kept for the backward (2 GB per layer at N = 2e6, H = 8, G = 32).
 The fused route has no CPU implementation: on CPU tensors its operators
@@ -26,6 +27,7 @@ import logging
 import torch
 import torch.nn as nn
 
+from ..kernels.coupling import fused_coupling
 from ..kernels.slice_ops import fused_deslice, fused_slice, unsupported_dims
 from .basic import PointLinear
 
@@ -104,14 +106,20 @@ class Physics_Attention_Irregular_Mesh(nn.Module):  # noqa: N801 (reference name
         fx_mid = self.in_project_fx(x).view(B, N, H, D)
         tau = self.temperature.view(H)
         W, b = self.in_project_slice.weight, self.in_project_slice.bias
-        z_num, s, stats = fused_slice(x_mid, fx_mid, W, b, tau, return_stats=True)
-        tokens = self._mix_tokens(z_num / (s + TOKEN_EPS).unsqueeze(-1))
         if self.untied_deslice:
+            z_num, s = fused_slice(x_mid, fx_mid, W, b, tau)
+            tokens = self._mix_tokens(z_num / (s + TOKEN_EPS).unsqueeze(-1))
             out = fused_deslice(x_mid, self.in_project_deslice.weight,
                                 self.in_project_deslice.bias,
                                 self.deslice_temperature.view(H), tokens)
         else:
-            out = fused_deslice(x_mid, W, b, tau, tokens, stats=stats)
+            # slice and deslice on one x_mid, W, b, tau: one coupling, whose
+            # backward is one merged pass (the deslice's dx, dW, db, dtau
+            # formed in the slice's backward) and no autograd sum of two dx
+            c = fused_coupling(x_mid, W, b, tau)
+            z_num, s = c.slice(fx_mid)
+            tokens = self._mix_tokens(z_num / (s + TOKEN_EPS).unsqueeze(-1))
+            out = c.deslice(tokens)
         return self.to_out(out.reshape(B, N, H * D)), None
 
     def forward(self, x, slice_weights_in=None):

@@ -80,8 +80,9 @@ typedef struct fs_slice_params {
    * of every point tensor, whose stride_b is then ignored. Device memory,
    * B + 1 non-decreasing int64 with row_splits[0] = 0 and no sample longer
    * than N (N sizes the launch; it is not read from the device). Served by
-   * the whole-G family only, without statistics (stats_in / stats_out must
-   * be NULL; fs_compute_stats refuses it): FS_ERR_UNSUPPORTED otherwise.
+   * both kernel families; the statistics of a ragged batch (stats_in,
+   * stats_out, fs_compute_stats) are (1, H, 2, total_rows) fp32, indexed by
+   * row. Slot sums and parameter gradients stay per sample (B, H, ...).
    * No counterpart in the reference, whose ROADMAP.md:66-68 plans it.
    * The library never reads the splits on the host (that would synchronise):
    * the kernels clamp every split to [0, total_rows] and every sample to N

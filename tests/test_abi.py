@@ -157,9 +157,10 @@ def _pts(t, width):
 
 
 def test_tied_and_row_splits_refused_before_launch():
-    """fs_tied_bwd serves the whole-G family only; row splits refuse the
-    G-blocked family and statistics. All of it is decided before a launch
-    (the host buffers passed here are never touched)."""
+    """fs_tied_bwd serves the whole-G family only; row splits need their
+    total rows, and are served with statistics and by the G-blocked family.
+    All of it is decided before a launch (the host buffers passed here are
+    never touched)."""
     lib = _hip.lib()
     buf = torch.zeros(64)
     x = _pts(buf, 32)
@@ -178,14 +179,20 @@ def test_tied_and_row_splits_refused_before_launch():
                             None, None, ctypes.byref(x), None, 0, None)
     assert rc == _hip.FS_ERR_INVALID and b"total_rows" in lib.fs_last_error()
     p.total_rows = 100
+    # row splits are served with statistics and by the G-blocked family: these
+    # calls pass validation and stop at the (missing) workspace
     rc = lib.fs_slice_fwd(ctypes.byref(x), ctypes.byref(x), ctypes.byref(p), None,
                           ctypes.c_void_p(buf.data_ptr()), ctypes.c_void_p(buf.data_ptr()),
                           ctypes.c_void_p(buf.data_ptr()), None, 0, None)
-    assert rc == _hip.FS_ERR_UNSUPPORTED and b"statistics" in lib.fs_last_error()
+    assert rc == _hip.FS_ERR_WORKSPACE
+    p.family = 2
     rc = lib.fs_compute_stats(ctypes.byref(x), ctypes.byref(p), ctypes.c_void_p(buf.data_ptr()),
                               0, None, 0, None)
-    assert rc == _hip.FS_ERR_UNSUPPORTED and b"row splits" in lib.fs_last_error()
-    p.family = 2
+    assert rc == _hip.FS_ERR_WORKSPACE
     rc = lib.fs_deslice_fwd(ctypes.byref(x), ctypes.byref(p), ctypes.c_void_p(buf.data_ptr()),
                             None, None, ctypes.byref(x), None, 0, None)
-    assert rc == _hip.FS_ERR_UNSUPPORTED and b"whole-G" in lib.fs_last_error()
+    assert rc == _hip.FS_ERR_WORKSPACE
+    # a ragged batch's per-point buffers are sized by its total rows, H planes
+    nws = lib.fs_workspace_bytes(_hip.OP_DESLICE_BWD, ctypes.byref(p))
+    p.total_rows = 100_000
+    assert lib.fs_workspace_bytes(_hip.OP_DESLICE_BWD, ctypes.byref(p)) > nws + 3 * 2 * 99_900 * 4

@@ -345,3 +345,22 @@ def test_coupling_compile_keeps_one_graph(order):
                                            m(3), m(2, 3, 5, 8), m(8, 8))
     assert explain.graph_break_count == 0, explain.break_reasons
     assert explain.graph_count == 1
+
+
+def test_varlen_statistics_layout():
+    """A ragged batch's statistics are (1, H, 2, rows), indexed by row, on
+    both routes (G <= 128 and the G-blocked G > 128); either op accepts the
+    other's."""
+    from flashslice_amd.kernels import fused_deslice_varlen, fused_slice_varlen
+    m = lambda *s: torch.empty(*s, device="meta", requires_grad=True)  # noqa: E731
+    for G in (32, 256):
+        x, fx, W, b, tau, tok = m(100, 4, 32), m(100, 4, 32), m(4, G, 32), m(4, G), m(4), \
+            m(3, 4, G, 32)
+        rs = [0, 40, 40, 100]
+        z, s, st = fused_slice_varlen(x, fx, W, b, tau, rs, return_stats=True)
+        assert st.shape == (1, 4, 2, 100) and st.dtype == torch.float32
+        out, st2 = fused_deslice_varlen(x, W, b, tau, tok, rs, stats=st, return_stats=True)
+        assert out.shape == (100, 4, 32) and st2.shape == st.shape
+        z, s = fused_slice_varlen(x, fx, W, b, tau, rs, stats=st2)
+        gs = torch.autograd.grad(z.sum() + s.sum() + out.sum(), [x, fx, W, b, tau, tok])
+        assert [g.shape for g in gs] == [t.shape for t in (x, fx, W, b, tau, tok)]

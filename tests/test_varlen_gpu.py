@@ -1,5 +1,6 @@
 """Parity of ragged batches (``fused_slice_varlen`` / ``fused_deslice_varlen``,
-row splits through the whole-G kernels) on the GPU.
+row splits through both kernel families, with and without the statistics
+handed from the slice to the deslice) on the GPU.
 
 One launch covers samples of different point counts -- including an empty
 sample and a one-point sample. Each sample's slice sums, deslice rows and
@@ -36,18 +37,21 @@ def _inputs(lens, H, D, DV, G, layout, seed=3):
     return L, tm, up
 
 
-def _run(L, tm, up, lens, layout, dtype, device, fused):
-    """slice -> tokens = (z / (s + eps)) @ tm -> deslice, per sample or ragged;
-    the loss contracts out, z_num, s with the upstream gradients."""
+def _run(L, tm, up, lens, layout, dtype, device, fused, tied=False):
+    """slice -> tokens = (z / (s + eps)) @ tm -> deslice, per sample or ragged
+    (``tied``: the slice's statistics handed to the deslice); the loss
+    contracts out, z_num, s with the upstream gradients."""
     T = {k: v.detach().to(device=device, dtype=dtype).requires_grad_(True) for k, v in L.items()}
     tmd = tm.to(device=device, dtype=dtype)
     splits = [0]
     for n in lens:
         splits.append(splits[-1] + n)
     if fused:
-        z, s = fused_slice_varlen(T["x"], T["fx"], T["w"], T["b"], T["tau"], splits)
+        z, s, st = fused_slice_varlen(T["x"], T["fx"], T["w"], T["b"], T["tau"], splits,
+                                      return_stats=True)
         tok = (z / (s + oracle.EPS_TOKEN)[..., None]) @ tmd
-        out = fused_deslice_varlen(T["x"], T["w"], T["b"], T["tau"], tok, splits)
+        out = fused_deslice_varlen(T["x"], T["w"], T["b"], T["tau"], tok, splits,
+                                   stats=st if tied else None)
     else:
         zs, ss, outs = [], [], []
         for i in range(len(lens)):
@@ -69,19 +73,33 @@ def _run(L, tm, up, lens, layout, dtype, device, fused):
 
 
 CASES = [
-    ("hgd-d32-g32", [1000, 0, 1, 3001, 517], 8, 32, 32, 32, "hgd"),
-    ("bhgd-dv64-g64", [2048, 33, 0, 700], 4, 32, 64, 64, "bhgd"),
-    ("gd-masked-g40-d40-dv24", [129, 1537, 64], 4, 40, 24, 40, "gd"),
+    # name, sample lengths, H, D, DV, G, weight layout, kernel mode
+    ("hgd-d32-g32", [1000, 0, 1, 3001, 517], 8, 32, 32, 32, "hgd", "auto"),
+    ("bhgd-dv64-g64", [2048, 33, 0, 700], 4, 32, 64, 64, "bhgd", "auto"),
+    ("gd-masked-g40-d40-dv24", [129, 1537, 64], 4, 40, 24, 40, "gd", "auto"),
+    # the G-blocked kernels: prepared-fragment (D, DV <= 64) and wide
+    ("hgd-g256-blocked", [1000, 0, 1, 3001, 517], 4, 32, 32, 256, "hgd", "auto"),
+    ("bhgd-g1024-blocked", [700, 1, 0, 1500], 2, 32, 32, 1024, "bhgd", "auto"),
+    ("hgd-g48-masked-blocked", [129, 0, 1537], 4, 32, 32, 48, "hgd", "blocked"),
+    ("hgd-d128-dv96-g64-wide", [300, 0, 1, 1029], 2, 128, 96, 64, "hgd", "auto"),
+    ("gd-g32-forced-blocked", [1000, 0, 1, 2049], 4, 32, 32, 32, "gd", "blocked"),
 ]
 
 
-@pytest.mark.parametrize("name,lens,H,D,DV,G,layout", CASES, ids=[c[0] for c in CASES])
-def test_varlen_parity(name, lens, H, D, DV, G, layout):
+@pytest.mark.parametrize("tied", [False, True], ids=["own-stats", "tied-stats"])
+@pytest.mark.parametrize("name,lens,H,D,DV,G,layout,kmode", CASES, ids=[c[0] for c in CASES])
+def test_varlen_parity(name, lens, H, D, DV, G, layout, kmode, tied):
+    from flashslice_amd.kernels import set_kernel_mode
     L, tm, up = _inputs(lens, H, D, DV, G, layout)
     ref = _run(L, tm, up, lens, layout, torch.float64, "cpu", False)
     ea = _run(L, tm, up, lens, layout, torch.float32, "cpu", False)
-    fu = _run(L, tm, up, lens, layout, torch.float32, "cuda", True)
-    fu2 = _run(L, tm, up, lens, layout, torch.float32, "cuda", True)
+    set_kernel_mode(kmode)
+    try:
+        fu = _run(L, tm, up, lens, layout, torch.float32, "cuda", True, tied)
+        fu2 = _run(L, tm, up, lens, layout, torch.float32, "cuda", True, tied)
+    finally:
+        set_kernel_mode("auto")
+    blocked = G > 128 or kmode == "blocked" or max(D, DV) > 64
     fails = []
     print("\ncase", name, flush=True)
     for k in ref:
@@ -89,7 +107,9 @@ def test_varlen_parity(name, lens, H, D, DV, G, layout):
         print("  %-10s eager %.3e  fused %.3e  fused-vs-eager %.3e" % (k, ee, ef, fe))
         if fu[k].shape != ea[k].shape or fu[k].dtype != ea[k].dtype:
             fails.append("%s shape/dtype" % k)
-        ok = ef <= 1.25 * ee + 1e-6 or (ee > 1e-4 and ef <= 3.0 * ee)
+        # dtau at 2x on the G-blocked kernels (reference bench/parity_ops.py:190-200)
+        g = 2.0 if (k == "grad:tau" and blocked) else 1.25
+        ok = ef <= g * ee + 1e-6 or (ee > 1e-4 and ef <= 3.0 * ee)
         if ok and ee < 1e-5 and fe > 1e-5 + ee:
             ok = False
         if not ok:
@@ -151,10 +171,10 @@ def test_varlen_bench_shape():
     rs = torch.tensor(splits, dtype=torch.int64).cuda()
     ops = torch.ops.flashslice
     nmax = max(lens)
-    z, s = ops.slice_varlen(x, fx, W, b, tau, rs, nmax, 0)
-    out = ops.deslice_varlen(x, W, b, tau, tok, rs, nmax, 0)
-    dx, dfx, _, _, _ = ops.slice_varlen_bwd(x, fx, W, b, tau, rs, nmax, dz, ds, 0)
-    z2, s2 = ops.slice_varlen(x, fx, W, b, tau, rs, nmax, 0)
+    z, s, st = ops.slice_varlen(x, fx, W, b, tau, rs, nmax, None, 0)
+    out, _ = ops.deslice_varlen(x, W, b, tau, tok, rs, nmax, st, 0)
+    dx, dfx, _, _, _ = ops.slice_varlen_bwd(x, fx, W, b, tau, rs, nmax, st, dz, ds, 0)
+    z2, s2, _ = ops.slice_varlen(x, fx, W, b, tau, rs, nmax, None, 0)
     assert torch.equal(z, z2) and torch.equal(s, s2)
     # the public API with device row splits (trusted, max_rows given) and
     # with host row splits (validated, copied) launch the same kernels
@@ -170,3 +190,28 @@ def test_varlen_bench_shape():
         assert relerr(z[i], z1[0]) < 1e-5 and relerr(s[i], s1[0]) < 1e-5, i
         assert torch.equal(out[sl], o1[0]), i
         assert relerr(dx[sl], dx1[0]) < 1e-5 and relerr(dfx[sl], dfx1[0]) < 1e-5, i
+
+
+@pytest.mark.parametrize("G", [32, 256], ids=["whole-g", "g-blocked"])
+def test_varlen_statistics_match_oracle(G):
+    """A ragged batch's statistics (1, H, 2, rows), row by row, against the
+    oracle's per sample, from the slice and from the online deslice."""
+    lens, H, D = [700, 0, 1, 1500], 4, 32
+    L, _, _ = _inputs(lens, H, D, D, G, "hgd")
+    dev = {k: v.cuda() for k, v in L.items()}
+    splits = [0, 700, 700, 701, 2201]
+    tok = torch.randn(4, H, G, D).cuda()
+    _, _, st = fused_slice_varlen(dev["x"], dev["fx"], dev["w"], dev["b"], dev["tau"], splits,
+                                  return_stats=True)
+    _, st2 = fused_deslice_varlen(dev["x"], dev["w"], dev["b"], dev["tau"], tok, splits,
+                                  return_stats=True)
+    assert st.shape == (1, H, 2, 2201) and st2.shape == st.shape
+    for i in range(4):
+        a, b_ = splits[i], splits[i + 1]
+        if a == b_:
+            continue
+        ref = oracle.stats(L["x"][a:b_].unsqueeze(0).double(), L["w"].double(),
+                           L["b"].double(), L["tau"].double())
+        for got in (st, st2):
+            assert relerr(got[:, :, 0, a:b_], ref[:, :, 0]) < 1e-6
+            assert relerr(got[:, :, 1, a:b_], ref[:, :, 1]) < 1e-5
