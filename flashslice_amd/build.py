@@ -25,7 +25,8 @@ LIB_PATH = os.path.join(OUT_DIR, LIB_NAME)
 BUILD_DIR = os.path.join(os.path.dirname(HERE), "_build")
 
 ARCH = "gfx950"
-SOURCES = ("fs_fused.hip", "fs_blocked.hip", "fs_reduce.hip", "fs_layernorm.hip", "fs_abi.cpp")
+SOURCES = ("fs_fused.hip", "fs_blocked.hip", "fs_coop.hip", "fs_reduce.hip", "fs_layernorm.hip",
+           "fs_abi.cpp")
 # explicit instances of fused_launch<K, T, DK> (fs_fused_kernels.h), one
 # generated translation unit each so that they compile in parallel
 _FUSED_TYPES = (("float", (0,)), ("__bf16", (0, 1, 2)), ("_Float16", (0, 1, 2)))

@@ -100,6 +100,27 @@ Geo geo_g(const fs_slice_params* p, int dk) {
   return geo_n(p, (t + nsg - 1) / nsg);
 }
 
+// The block-cooperative G-blocked kernels (fs_coop_kernels.h): bf16 dots
+// (dot kind 2) on 16-bit point tensors at 128 < G <= 256, D, DV <= 32. One
+// 8-wave block per CU (86 KB of LDS, two waves per SIMD), so the grid targets
+// one block per CU; P = blocks per (b, h), at most the G-blocked slot-owned
+// grid's partitions, whose partial buffer it reuses (one partial per block).
+constexpr int64_t kCoopBlocks = 256;
+bool coop_on(const fs_slice_params* p, int mode) {
+  return mode == 2 && fs::coop_ok((int)p->G, (int)p->D, (int)p->DV);
+}
+Geo geo_coop(const fs_slice_params* p) {
+  Geo g;
+  g.ntiles = (int)((p->N + fs::kTile - 1) / fs::kTile);
+  const int64_t bh = p->B * p->H;
+  int64_t P = (kCoopBlocks + bh - 1) / bh;
+  if (P > g.ntiles) P = g.ntiles;
+  if (P < 1) P = 1;
+  const int64_t cap = geo_g(p, -1).P;
+  g.P = (int)(P < cap ? P : cap);
+  return g;
+}
+
 // Blocks per launch of the whole-G kernels (measured on MI355X at C2: N = 1e6,
 // H = 8, D = DV = G = 32, and at C4: G = 64, DV = 64): at C2's shape the
 // kernels run best with several times more blocks than stay resident, so
@@ -470,6 +491,19 @@ int32_t slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_params
     a.part = ws.part;
     a.stats_out = stats_out;
     rc = hip_check(fs::launch_fused_slice_fwd(a, x->dtype, mode, st), who);
+  } else if (coop_on(p, mode)) {
+    // one pass: the statistics from stats_in, or formed in the pass
+    g = geo_coop(p);
+    fs::Args a = base_args(p, g);
+    set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_in(p, fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
+    a.vec_x = vec_ok(x);
+    a.vec_f = vec_ok(fx);
+    a.fast = a.vec_x && a.vec_f && full_widths(p);
+    a.part = ws.part;
+    a.stats_in = stats_in;
+    a.stats_out = stats_in ? nullptr : stats_out;
+    rc = hip_check(fs::launch_coop(fs::CK_SLICE_FWD, a, x->dtype, st), who);
   } else {
     g = geo_g(p, mode);
     fs::Args a = base_args(p, g);
@@ -492,7 +526,7 @@ int32_t slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_params
     rc = hip_check(fs::launch_blocked(fs::BK_SLICE_G, a, x->dtype, mode, st), who);
   }
   if (rc) return rc;
-  // partials: one per block (whole-G) or per wave (G-blocked)
+  // partials: one per block (whole-G, cooperative) or per wave (G-blocked)
   const int np = family_of(p) == 1 ? pb(g) : g.P;
   fs::ReduceSegments rs{};
   rs.seg[0] = seg(ws.part, wf, 0, np, G * DV, (int)p->B, (int)p->H, z_num);
@@ -665,15 +699,31 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     a.fast = a.vec_x && a.vec_f && a.vec_1 && a.vec_2 && full_widths(p);
     a.tok = dz_num;
     a.ds = ds;
-    rc = gp_prepare(a, p, ws, mode, st, who);
-    if (rc) return rc;
+    const bool coop = coop_on(p, mode);
     const float* stats = stats_in;
+    if (!coop || !stats) {
+      rc = gp_prepare(a, p, ws, mode, st, who);
+      if (rc) return rc;
+    }
     if (!stats) {
       rc = run_stats(x, p, ws.stats, 0, a, st, who);
       if (rc) return rc;
       stats = ws.stats;
     }
     a.stats_in = stats;
+    if (coop) {
+      // one pass from the statistics: dfx, dx, and dW, db, dtau per block
+      const Geo gc = geo_coop(p);
+      a.P = gc.P;
+      a.part = ws.part;
+      rc = hip_check(fs::launch_coop(fs::CK_SLICE_BWD, a, x->dtype, st), who);
+      if (rc) return rc;
+      rs.seg[0] = seg(ws.part, wf, 0, gc.P, G * D, Bw, Hw, dweight);
+      rs.seg[1] = seg(ws.part, wf, (int64_t)G * D, gc.P, G, Bb, Hb, dbias);
+      rs.seg[2] = seg(ws.part, wf, (int64_t)G * D + G, gc.P, 1, 1, (int)p->H, dtau);
+      rs.n = 3;
+      return hip_check(fs::launch_reduce((int)p->B, (int)p->H, rs, st), who);
+    }
     a.delta = ws.delta;
     a.lsum = ws.lsum;
     a.part2 = ws.part2;
@@ -747,14 +797,31 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
     a.vec_1 = vec_ok(dx);
     a.fast = a.vec_x && a.vec_f && a.vec_1 && full_widths(p);
     a.tok = tokens;
-    rc = gp_prepare(a, p, ws, mode, st, who);
-    if (rc) return rc;
+    const bool coop = coop_on(p, mode);
+    if (!coop || !stats) {
+      rc = gp_prepare(a, p, ws, mode, st, who);
+      if (rc) return rc;
+    }
     if (!stats) {
       rc = run_stats(x, p, ws.stats, 0, a, st, who);
       if (rc) return rc;
       stats = ws.stats;
     }
     a.stats_in = stats;
+    if (coop) {
+      // one pass from the statistics: dx, and dtokens, dW, db, dtau per block
+      const Geo gc = geo_coop(p);
+      a.P = gc.P;
+      a.part = ws.part;
+      rc = hip_check(fs::launch_coop(fs::CK_DESLICE_BWD, a, x->dtype, st), who);
+      if (rc) return rc;
+      rs.seg[0] = seg(ws.part, wf, 0, gc.P, G * DV, (int)p->B, (int)p->H, dtokens);
+      rs.seg[1] = seg(ws.part, wf, offW, gc.P, G * D, Bw, Hw, dweight);
+      rs.seg[2] = seg(ws.part, wf, offB, gc.P, G, Bb, Hb, dbias);
+      rs.seg[3] = seg(ws.part, wf, offB + G, gc.P, 1, 1, (int)p->H, dtau);
+      rs.n = 4;
+      return hip_check(fs::launch_reduce((int)p->B, (int)p->H, rs, st), who);
+    }
     a.delta = ws.delta;
     a.lsum = ws.lsum;
     a.part2 = ws.part2;

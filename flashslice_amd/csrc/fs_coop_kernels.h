@@ -1,0 +1,508 @@
+// Block-cooperative kernels of the G-blocked family: bf16 dots (dot kind 2),
+// 128 < G <= 256, D and DV <= 32 (config 3's G = 256 in bf16).
+//
+// The G-blocked kernels split a pass into a point-owned and a slot-owned
+// kernel and carry the normalisation between them through per-point
+// buffers: every (point, slot) weight is recomputed in each of them (nine
+// exponentials per step at config 3) and every point tile is read once per
+// 32-slot block. Here a block of eight waves takes one point tile at a time
+// and wave w owns slots 32 w .. 32 w + 31, so the whole slot axis of the tile
+// is in the block's registers at once. What a point needs from every slot is
+// combined across the waves through LDS -- the softmax max and sum (slice
+// forward without statistics), delta = sum_g w omega (backward), and the
+// per-point outputs dx and dfx, each wave's partial over its own slots summed
+// in a fixed wave order -- and what a slot needs from every point stays in its
+// wave (z_num, s, dW, db, dtokens). Each op is one pass with one exponential
+// per (point, slot), and each point tile is read from HBM once.
+//
+// Each point tile is loaded once per block: 256 threads load it (16 bytes
+// each) while the previous tile is computed and store it in LDS as bf16 rows
+// in the transposable layout of tr_put, three buffers deep; the waves read
+// their MFMA operands from there, plain ([point, column]) or transposed
+// (ds_read_b64_tr_b16), with no fp32 round trip. Per tile, a slice forward
+// waits at one block barrier (the next tile and, without statistics, the
+// waves' (max, sum) pairs), a backward at two (the next tile and delta; the
+// dx / dfx exchange). The tile loop is identical in every wave of a block,
+// so the barriers are uniform.
+#pragma once
+#include "fs_device.h"
+#include "fs_internal.h"
+#include "fs_io.h"
+#include "fs_mma.h"
+#include "fs_tile.h"
+
+namespace fs {
+
+constexpr int kCoopWaves = 8;
+constexpr int kCoopThreads = 64 * kCoopWaves;
+constexpr int kCoopStride = 36;                  // staging row stride (floats), conflict-free
+constexpr int kCoopTr = kTrPieceB / 4;           // the wave's transpose region (floats)
+constexpr int kCoopX = 16 * 64;                  // one f32x16 per lane (floats)
+// per wave: during the prologue the fp32 staging of its 32 rows of W and of
+// tokens / dz_num; in the tile loop the transpose region and two exchange
+// fragments (dx, dfx)
+constexpr int kCoopWReg = kCoopTr + 2 * kCoopX;
+static_assert(2 * 32 * kCoopStride <= kCoopWReg, "coop staging exceeds the wave region");
+constexpr int kCoopPts = 4 * kCoopWaves * 32;    // per-point exchange: 2 buffers x 2 rows per wave
+constexpr int kCoopVec = 2 * 32 * kCoopWaves;    // per-slot vectors: bias * cst, d s
+constexpr int kCoopTileB = kTrPieceB;            // one staged 32 x 32 bf16 tile (bytes)
+constexpr int kCoopTiles = 3 * 2 * kCoopTileB / 4;  // 3 buffers x (x, fx / d_out) (floats)
+constexpr int kCoopLds = kCoopWaves * kCoopWReg + kCoopPts + kCoopVec + kCoopTiles;
+
+// the shapes these kernels serve (the host picks them for dot kind 2)
+__host__ __device__ inline bool coop_serves(int G, int D, int DV) {
+  return G > 128 && G <= 32 * kCoopWaves && D <= 32 && DV <= 32;
+}
+
+// Stage a (R x C) fp32 matrix (row stride C), zero-padded to 32 x 32, into
+// LDS with row stride kCoopStride; the 64 lanes of one wave.
+__device__ __forceinline__ void coop_stage(float* dst, const float* src, int R, int C, int lane) {
+  for (int i = lane; i < 32 * 32; i += 64) {
+    const int r = i >> 5, col = i & 31;
+    dst[r * kCoopStride + col] = (r < R && col < C) ? src[(int64_t)r * C + col] : 0.f;
+  }
+}
+
+// Sum over the 32 point lanes of each lane half of a per-lane [point, slot]
+// accumulator (16 registers): slot kmap(j, h) of the wave's 32. Through the
+// wave's LDS region; lane t < 32 returns slot t's sum (fixed order).
+__device__ __forceinline__ float coop_point_sum(const float (&v)[16], float* reg, int lane) {
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int j = 0; j < 16; ++j) reg[lane * 17 + j] = v[j];
+  __builtin_amdgcn_wave_barrier();
+  float s = 0.f;
+  if (lane < 32) {
+    const int hs = (lane >> 2) & 1, j = ((lane >> 3) << 2) | (lane & 3);
+    for (int p = 0; p < 32; ++p) s += reg[(p + 32 * hs) * 17 + j];
+  }
+  __builtin_amdgcn_wave_barrier();
+  return s;
+}
+
+#define COOP_PROLOGUE                                                                   \
+  __shared__ __attribute__((aligned(16))) float smem[kCoopLds];                         \
+  constexpr int M = MMA_BF16;                                                           \
+  const int lane = threadIdx.x & 63;                                                    \
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);                     \
+  const int c = lane & 31, h = lane >> 5;                                               \
+  const int bh = blockIdx.y;                                                            \
+  const int b = bh / a.H, hd = bh - b * a.H;                                            \
+  const Rows R_ = rows_of(a, b, hd);                                                    \
+  const int64_t row0_ = R_.row0;                                                        \
+  const int N = R_.N, ntiles_ = R_.ntiles;                                              \
+  const int G = a.G, D = a.D, DV = a.DV;                                                \
+  const int g0 = 32 * wid;                                                              \
+  const int pid = blockIdx.x;                                                           \
+  float* wreg = smem + wid * kCoopWReg;                                                 \
+  char* trS = reinterpret_cast<char*>(wreg);                                            \
+  float* xpt = smem + kCoopWaves * kCoopWReg;                                           \
+  float* sBC = xpt + kCoopPts;                                                          \
+  float* sDS = sBC + 32 * kCoopWaves;                                                   \
+  char* tiles_ = reinterpret_cast<char*>(sDS + 32 * kCoopWaves);                        \
+  const float tauf = a.tau[hd];                                                         \
+  const float cst = (float)(1.4426950408889634 / (double)tauf);                        \
+  const float inv_tau = 1.f / tauf;                                                     \
+  const bool fast = a.fast != 0;                                                        \
+  const float* Wp = a.W + b * a.swb + hd * a.swh;                                       \
+  const float* Bp = a.bias + b * a.sbb + hd * a.sbh;                                    \
+  const int Rw = G - g0 < 32 ? G - g0 : 32;                                             \
+  coop_stage(wreg, Wp + (int64_t)g0 * D, Rw, D, lane);                                  \
+  if (a.tok)                                                                            \
+    coop_stage(wreg + 32 * kCoopStride, a.tok + ((int64_t)bh * G + g0) * DV, Rw, DV, lane); \
+  if (lane < 32) {                                                                      \
+    const int g = g0 + lane;                                                            \
+    sBC[g0 + lane] = g < G ? Bp[g] * cst : kNoSlot;                                     \
+    sDS[g0 + lane] = (a.ds && g < G) ? a.ds[(int64_t)bh * G + g] : 0.f;                \
+  }                                                                                     \
+  __syncthreads();                                                                      \
+  Frag<M> qL; /* W [g, d]: the logits operand */                                       \
+  {                                                                                     \
+    float f_[16];                                                                       \
+    lds_frag_rowouter(f_, wreg, kCoopStride, 0, 0, c, h);                               \
+    prep<M>(qL, f_);                                                                    \
+  }                                                                                     \
+  (void)inv_tau; (void)fast; (void)DV; (void)row0_;
+
+// Point slices of one (b, h) (as FS_SLICE): byte base from the sample's
+// first row, byte row stride, row width, this lane's row c.
+#define COOP_SLICE(NAME, PTR, SB, SN, SH, C)                                                \
+  const char* NAME##_b =                                                                  \
+      (const char*)(PTR) + (b * (SB) + row0_ * (SN) + hd * (SH)) * (int64_t)sizeof(T);    \
+  const int64_t NAME##_sn = (SN) * (int64_t)sizeof(T);                                    \
+  const int64_t NAME##_w = (int64_t)(C) * (int64_t)sizeof(T);                             \
+  const uint32_t NAME##_row = (uint32_t)(c * NAME##_sn);
+
+// scaled logits t2 = (x . W + b) log2(e) / tau of the wave's 32 slots
+#define COOP_LOGITS(T2, XQ)                                                             \
+  {                                                                                     \
+    const f32x16 s_ = mma<M>(qL, XQ, zero16());                                         \
+    float bc_[16];                                                                      \
+    lds_frag_vec(bc_, sBC + g0, h);                                                     \
+    _Pragma("unroll") for (int r = 0; r < 16; ++r) T2[r] = fmaf(s_[r], cst, bc_[r]);    \
+  }
+
+// ---------------------------------------------------------- staged tiles
+// Thread i < 128's share of one tile of a (B, N, H, C) 16-bit point slice:
+// row i / 4, columns 8 (i % 4) .. + 7 (16 bytes). Rows beyond the slice's
+// range and columns beyond C read as zero.
+template <typename T, bool FAST>
+__device__ __forceinline__ void coop_tile_load(uint32_t (&v)[4], Rsrc r, int64_t snb, int C,
+                                               int i) {
+  const int row = i >> 2, col0 = 8 * (i & 3);
+  const uint32_t off = (uint32_t)(row * snb) + (uint32_t)col0 * 2u;
+  if constexpr (FAST) {
+    const auto q = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kStream);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = q[e];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(r, col0 + 2 * e < C ? off + 4u * e : kOff,
+                                                               0, kStream);
+      const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(
+          r, col0 + 2 * e + 1 < C ? off + 4u * e + 2u : kOff, 0, kStream);
+      v[e] = (lo & 0xffffu) | (hi << 16);
+    }
+  }
+}
+__device__ __forceinline__ void coop_tile_store(char* region, const uint32_t (&v)[4], int i) {
+  const int row = i >> 2, col0 = 8 * (i & 3);
+  *reinterpret_cast<uint2*>(region + tr_off(row, col0)) = make_uint2(v[0], v[1]);
+  *reinterpret_cast<uint2*>(region + tr_off(row, col0 + 4)) = make_uint2(v[2], v[3]);
+}
+// The [row, column] fragment of a staged tile (the inverse of tr_put): lane
+// (c, h) row c, columns kmap(j, h).
+__device__ __forceinline__ void tile_rows(Frag<MMA_BF16>& f, const char* region, int c, int h) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const uint2 lo = *reinterpret_cast<const uint2*>(region + tr_off(c, 16 * s + 4 * h));
+    const uint2 hi = *reinterpret_cast<const uint2*>(region + tr_off(c, 16 * s + 8 + 4 * h));
+    f.q[s] = u32x4{lo.x, lo.y, hi.x, hi.y};
+  }
+}
+
+// Staging of the block's point tiles: threads 0..127 take x, 128..255 the
+// second stream (fx or d_out); three LDS buffers rotate, so the tile stored
+// for the next step never overwrites one a slower wave may still read.
+#define COOP_STAGING(FAST)                                                              \
+  const int tid_ = threadIdx.x, li_ = tid_ & 127;                                       \
+  const bool ldx_ = tid_ < 128, ldf_ = tid_ >= 128 && tid_ < 256;                       \
+  uint32_t stg_[4] = {0u, 0u, 0u, 0u};                                                  \
+  auto gload = [&](int t) {                                                             \
+    const int64_t p0 = (int64_t)t * kTile;                                              \
+    if (ldx_) coop_tile_load<T, FAST>(stg_, rows_rsrc(x_b, x_sn, x_w, p0, N), x_sn, D, li_); \
+    else if (ldf_)                                                                      \
+      coop_tile_load<T, FAST>(stg_, rows_rsrc(f_b, f_sn, f_w, p0, N), f_sn, DV, li_);   \
+  };                                                                                    \
+  auto tile_at = [&](int buf, int stream) -> char* {                                    \
+    return tiles_ + (2 * buf + stream) * kCoopTileB;                                    \
+  };                                                                                    \
+  auto lstore = [&](int buf) {                                                          \
+    if (ldx_ || ldf_) coop_tile_store(tile_at(buf, ldx_ ? 0 : 1), stg_, li_);           \
+  };
+
+// ------------------------------------------------------------------ slice fwd
+// z_num, s of the wave's slots. Exponentials against the wave's own row max;
+// with saved statistics each weight is rescaled to the row's max and sum,
+// else the waves' (max, sum) pairs are combined after the tile's barrier
+// (buffers alternate by tile parity, so a wave may write the next tile's
+// pair while another still reads this one's) and written to stats_out when
+// asked for.
+template <typename T>
+__global__ __launch_bounds__(kCoopThreads, 1) void k_coop_slice_fwd(Args a) {
+  COOP_PROLOGUE
+  __syncthreads();  // the staging area becomes the transpose region
+  f32x16 zacc = zero16();
+  float sacc[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
+  COOP_SLICE(x, a.x, a.sxb, a.sxn, a.sxh, D)
+  COOP_SLICE(f, a.f, a.sfb, a.sfn, a.sfh, DV)
+  (void)x_row; (void)f_row;
+  const float* sm = a.stats_in ? a.stats_in + R_.stats_off() : nullptr;
+  const float* st_m = a.stats_out ? a.stats_out + R_.stats_off() : nullptr;
+  const float* st_l = st_m ? st_m + R_.NS : nullptr;
+  auto run = [&](auto fast_c) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    COOP_STAGING(FAST)
+    auto body = [&](int t, int cur, auto par) {
+      const int64_t p0 = (int64_t)t * kTile;
+      const bool pv = p0 + c < N;
+      constexpr float sg = decltype(par)::sign;
+      Frag<M> xq;
+      tile_rows(xq, tile_at(cur, 0), c, h);
+      float t2[16];
+      COOP_LOGITS(t2, xq)
+      float m = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) m = fmaxf(m, t2[r]);
+      m = pair_max(m);
+      float e[16], ls = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        e[r] = __builtin_amdgcn_exp2f(t2[r] - m);
+        ls += e[r];
+      }
+      float* xb = xpt + (sg < 0.f ? 2 * kCoopWaves * 32 : 0);
+      if (!sm) {
+        ls = pair_sum(ls);
+        if (h == 0) {
+          xb[wid * 32 + c] = m;
+          xb[kCoopWaves * 32 + wid * 32 + c] = ls;
+        }
+      }
+      lstore(cur == 2 ? 0 : cur + 1);  // publish the next tile
+      __syncthreads();
+      gload(t + 2 * a.P);  // the tile after it, into the staging registers
+      float m2, l;
+      if (sm) {
+        m2 = ld_pt(pts_rsrc(sm, p0, N), c) * kLog2e;
+        l = ld_pt(pts_rsrc(sm + R_.NS, p0, N), c);
+      } else {
+        m2 = xb[c];
+#pragma unroll
+        for (int w = 1; w < kCoopWaves; ++w) m2 = fmaxf(m2, xb[w * 32 + c]);
+        l = 0.f;
+#pragma unroll
+        for (int w = 0; w < kCoopWaves; ++w)
+          l += xb[kCoopWaves * 32 + w * 32 + c] * __builtin_amdgcn_exp2f(xb[w * 32 + c] - m2);
+        if (wid == 0) store_stats_tile(st_m, st_l, p0, N, c, h, m2, l);
+      }
+      // w = exp2(t2 - m) exp2(m - m2) / l
+      const float inv = pv ? __builtin_amdgcn_exp2f(m - m2) / l : 0.f;
+      float w[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        w[r] = e[r] * inv;
+        sacc[r] += w[r];
+      }
+      // z_num += w^T fx: w read back transposed, carrying the tile's sign;
+      // fx^T straight from the staged tile
+      Frag<M> wq, wTq, fT;
+      prep<M>(wq, w);
+      tr_put<M>(trS, wq, c, h, sg < 0.f ? 0x80008000u : 0u);
+      tr_get<M>(wTq, trS, lane);
+      tr_get<M>(fT, tile_at(cur, 1), lane);
+      mma_acc<M>(zacc, fT, wTq, sg);
+    };
+    int t = pid, cur = 0;
+    gload(t);
+    lstore(0);
+    gload(t + a.P);
+    __syncthreads();
+    while (t < ntiles_) {
+      body(t, cur, TileEven());
+      t += a.P;
+      cur = cur == 2 ? 0 : cur + 1;
+      if (t >= ntiles_) break;
+      body(t, cur, TileOdd());
+      t += a.P;
+      cur = cur == 2 ? 0 : cur + 1;
+    }
+  };
+  if (fast) run(std::true_type()); else run(std::false_type());
+  // the block's partial: the wave's slots of z_num (rows g0 + c) and s
+  const int64_t E = part_floats_slice_fwd(G, DV);
+  float* pw = a.part + ((int64_t)bh * gridDim.x + blockIdx.x) * E;
+  const float s = coop_point_sum(sacc, wreg + kCoopTr, lane);
+  const int g = g0 + c;
+  if (g < G) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int v = kmap(r, h);
+      if (v < DV) pw[(int64_t)g * DV + v] = zacc[r];
+    }
+    if (h == 0) pw[(int64_t)G * DV + g] = s;
+  }
+}
+
+// ---------------------------------------------------------------- backward
+// One pass of the slice (SLICE) or deslice backward from saved statistics:
+// omega = fx . dz_num + d s (slice) or d_out . tokens (deslice); delta and
+// Lb = w (omega - delta) per point; dx = Lb W / tau and (slice) dfx =
+// w dz_num summed over the waves; dW, db, (deslice) dtokens and the dtau
+// row terms of the wave's slots.
+template <typename T, bool SLICE>
+__global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
+  COOP_PROLOGUE
+  Frag<M> qVr, qVc, qWc;  // V [g, v] (omega), V [v, g] (dfx), W / tau [d, g] (dx)
+  {
+    float f_[16];
+    lds_frag_rowouter(f_, wreg + 32 * kCoopStride, kCoopStride, 0, 0, c, h);
+    prep<M>(qVr, f_);
+    lds_frag_colouter(f_, wreg + 32 * kCoopStride, kCoopStride, 0, 0, c, h);
+    prep<M>(qVc, f_);
+    lds_frag_colouter(f_, wreg, kCoopStride, 0, 0, c, h);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) f_[j] *= inv_tau;
+    prep<M>(qWc, f_);
+  }
+  (void)qVc;
+  __syncthreads();  // the staging area becomes the transpose and exchange regions
+  f32x16 dW = zero16(), dT = zero16();
+  float dbacc[16], dtacc = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) dbacc[r] = 0.f;
+  COOP_SLICE(x, a.x, a.sxb, a.sxn, a.sxh, D)
+  COOP_SLICE(f, a.f, a.sfb, a.sfn, a.sfh, DV)
+  COOP_SLICE(dx, a.o1, a.s1b, a.s1n, a.s1h, D)
+  COOP_SLICE(df, a.o2, a.s2b, a.s2n, a.s2h, DV)
+  (void)x_row; (void)f_row; (void)dx_row; (void)df_row;
+  const uint32_t vcx = col_off<T>(0, D, dx_sn, c, h);
+  const uint32_t vcf = col_off<T>(0, DV, df_sn, c, h);
+  (void)vcf;
+  const float* sm = a.stats_in + R_.stats_off();
+  const float* sl = sm + R_.NS;
+  // registers 2 wid, 2 wid + 1 of the exchanged fragments are this wave's to
+  // sum and store (rows 4 h + tile_row(j) of the tile)
+  const int j0 = 2 * wid;
+  auto run = [&](auto fast_c) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    COOP_STAGING(FAST)
+    auto body = [&](int t, int cur, auto par) {
+      const int64_t p0 = (int64_t)t * kTile;
+      const bool pv = p0 + c < N;
+      constexpr float sg = decltype(par)::sign;
+      constexpr uint32_t neg = sg < 0.f ? 0x80008000u : 0u;
+      Frag<M> xq, fq;
+      tile_rows(xq, tile_at(cur, 0), c, h);
+      tile_rows(fq, tile_at(cur, 1), c, h);
+      float t2[16];
+      COOP_LOGITS(t2, xq)
+      const float m2 = ld_pt(pts_rsrc(sm, p0, N), c) * kLog2e;
+      const float l = ld_pt(pts_rsrc(sl, p0, N), c);
+      const float inv = pv ? 1.f / l : 0.f;
+      float w[16], om[16];
+      {
+        const f32x16 o = mma<M>(qVr, fq, zero16());
+        float dsv[16];
+        if (SLICE) lds_frag_vec(dsv, sDS + g0, h);
+        float d = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          t2[r] -= m2;
+          w[r] = __builtin_amdgcn_exp2f(t2[r]) * inv;
+          om[r] = SLICE ? o[r] + dsv[r] : o[r];
+          d += w[r] * om[r];
+        }
+        d = pair_sum(d);
+        if (h == 0) xpt[wid * 32 + c] = d;
+      }
+      Frag<M> wq;
+      prep<M>(wq, w);
+      if (!SLICE) {
+        // dtokens += w^T d_out: d_out^T straight from the staged tile, w
+        // read back transposed
+        Frag<M> oTq, wTq;
+        tr_get<M>(oTq, tile_at(cur, 1), lane);
+        tr_put<M>(trS, wq, c, h, neg);
+        tr_get<M>(wTq, trS, lane);
+        mma_acc<M>(dT, oTq, wTq, sg);
+      }
+      lstore(cur == 2 ? 0 : cur + 1);  // publish the next tile
+      __syncthreads();
+      gload(t + 2 * a.P);
+      float delta = 0.f;
+#pragma unroll
+      for (int wv = 0; wv < kCoopWaves; ++wv) delta += xpt[wv * 32 + c];
+      float rt = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float lb = w[r] * (om[r] - delta);
+        rt = fmaf(lb, t2[r], rt);
+        dbacc[r] += lb;
+        om[r] = lb;
+      }
+      rt = pair_sum(rt);
+      dtacc += (pv && h == 0) ? rt : 0.f;
+      Frag<M> lq;
+      prep<M>(lq, om);
+      // this wave's partials of dx (and dfx) for the exchange
+      {
+        const f32x16 px = mma<M>(lq, qWc, zero16());
+#pragma unroll
+        for (int r = 0; r < 16; ++r) wreg[kCoopTr + r * 64 + lane] = px[r];
+        if (SLICE) {
+          const f32x16 pf = mma<M>(wq, qVc, zero16());
+#pragma unroll
+          for (int r = 0; r < 16; ++r) wreg[kCoopTr + kCoopX + r * 64 + lane] = pf[r];
+        }
+      }
+      // dW += x^T Lb: x^T straight from the staged tile, Lb read back
+      // transposed
+      {
+        Frag<M> xTq, lTq;
+        tr_put<M>(trS, lq, c, h, neg);
+        tr_get<M>(lTq, trS, lane);
+        tr_get<M>(xTq, tile_at(cur, 0), lane);
+        mma_acc<M>(dW, xTq, lTq, sg);
+      }
+      __syncthreads();
+      // sum the eight waves' partials of this wave's two registers, fixed order
+      const Rsrc rdx = rows_rsrc(dx_b, dx_sn, dx_w, p0, N);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int j = j0 + q;
+        float s = 0.f;
+#pragma unroll
+        for (int wv = 0; wv < kCoopWaves; ++wv) s += smem[wv * kCoopWReg + kCoopTr + j * 64 + lane];
+        Buf<T>::st1(rdx, vcx + (uint32_t)tile_row(j) * (uint32_t)dx_sn, s);
+      }
+      if (SLICE) {
+        const Rsrc rdf = rows_rsrc(df_b, df_sn, df_w, p0, N);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int j = j0 + q;
+          float s = 0.f;
+#pragma unroll
+          for (int wv = 0; wv < kCoopWaves; ++wv)
+            s += smem[wv * kCoopWReg + kCoopTr + kCoopX + j * 64 + lane];
+          Buf<T>::st1(rdf, vcf + (uint32_t)tile_row(j) * (uint32_t)df_sn, s);
+        }
+      }
+    };
+    int t = pid, cur = 0;
+    gload(t);
+    lstore(0);
+    gload(t + a.P);
+    __syncthreads();
+    while (t < ntiles_) {
+      body(t, cur, TileEven());
+      t += a.P;
+      cur = cur == 2 ? 0 : cur + 1;
+      if (t >= ntiles_) break;
+      body(t, cur, TileOdd());
+      t += a.P;
+      cur = cur == 2 ? 0 : cur + 1;
+    }
+  };
+  if (fast) run(std::true_type()); else run(std::false_type());
+  // the block's partial: dW, db (and dtokens) of the wave's slots; dtau of
+  // the block (the waves' row terms summed in a fixed order)
+  const float dtw = half_wave_sum(dtacc);
+  __syncthreads();
+  if (lane == 0) xpt[wid] = dtw;
+  const float db = coop_point_sum(dbacc, wreg + kCoopTr, lane) * inv_tau;
+  __syncthreads();
+  const int g = g0 + c;
+  const int64_t E = SLICE ? part_floats_slice_bwd(G, D) : part_floats_deslice_bwd(G, D, DV);
+  const int64_t offW = SLICE ? 0 : (int64_t)G * DV, offB = offW + (int64_t)G * D;
+  float* pw = a.part + ((int64_t)bh * gridDim.x + blockIdx.x) * E;
+  if (g < G) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = kmap(r, h);
+      if (d < D) pw[offW + (int64_t)g * D + d] = dW[r] * inv_tau;
+      if (!SLICE && d < DV) pw[(int64_t)g * DV + d] = dT[r];
+    }
+    if (h == 0) pw[offB + g] = db;
+  }
+  if (wid == 0 && lane == 0) {
+    float dt = 0.f;
+    for (int wv = 0; wv < kCoopWaves; ++wv) dt += xpt[wv];
+    pw[offB + G] = -kLn2 * inv_tau * dt;
+  }
+}
+
+}  // namespace fs

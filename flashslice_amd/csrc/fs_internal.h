@@ -162,6 +162,15 @@ hipError_t launch_blocked(int kind, const Args& a, int dtype, int mode, hipStrea
 hipError_t launch_gp_prep(const Args& a, int mode, hipStream_t st);
 int blocked_width_blocks(int D, int DV);  // 1, 2, 4 or 8 (0 if D or DV > 256)
 
+// Block-cooperative kernels of the G-blocked family (fs_coop.hip): bf16 dots
+// on 16-bit point tensors, 128 < G <= 256, D, DV <= 32 (coop_serves). A block
+// of eight waves takes one point tile at a time, wave w slots 32 w ..; grid
+// (P, B * H) with a.P = the blocks per (b, h); one partial per block in the
+// whole-G layout (part_floats_*). The backward kernels need statistics.
+enum CoopKind { CK_SLICE_FWD = 0, CK_SLICE_BWD = 1, CK_DESLICE_BWD = 2 };
+hipError_t launch_coop(int kind, const Args& a, int dtype, hipStream_t st);
+bool coop_ok(int G, int D, int DV);
+
 // Deterministic reduction of per-wave partials (fs_reduce.hip). One output
 // segment: out[ob][oh][e] = sum over the contributing waves (b -> ob =
 // Bo > 1 ? b : 0, h -> oh = Ho > 1 ? h : 0, every partition p < P) of

@@ -214,3 +214,27 @@ def test_stats_modes_agree():
     ref = oracle.stats(*(t.double().cpu() for t in (x, w, b, tau)))
     assert relerr(st_two[:, :, 0], ref[:, :, 0]) < 1e-6
     assert relerr(st_two[:, :, 1], ref[:, :, 1]) < 1e-5
+
+
+# ------------------------------------------------ block-cooperative kernels
+# bf16 dots on bf16 point tensors at 128 < G <= 256 (D, DV <= 32) run the
+# G-blocked family's block-cooperative kernels (slice forward and both
+# backward passes in one pass each); these cases cover partial last waves
+# (G not a multiple of 32 * 8), narrow widths, tiny N, both call orders
+# (statistics formed in the slice's pass, or handed in by the deslice) and
+# per-sample weights, against the same gates as every bf16 case.
+COOP = [
+    ("coop-g256-hgd", dict(B=1, N=4097, H=4, D=32, G=256, mode="hgd"), "slice-first"),
+    ("coop-g160-gd-deslice-first", dict(B=2, N=1025, H=4, D=32, G=160, mode="gd"),
+     "deslice-first"),
+    ("coop-g200-d24-dv16", dict(B=1, N=2049, H=2, D=24, DV=16, G=200, mode="hgd"),
+     "slice-first"),
+    ("coop-g256-bhgd-tinyN17", dict(B=2, N=17, H=4, D=32, G=256, mode="bhgd"), "slice-first"),
+]
+
+
+@pytest.mark.parametrize("name,kw,order", COOP, ids=[c[0] for c in COOP])
+def test_coop_bf16_parity(name, kw, order):
+    fails, rows = check_case(Case(**kw), order=order, dot="bf16", blocked=True)
+    _report(name, fails, rows)
+    bf16_gate(rows)
