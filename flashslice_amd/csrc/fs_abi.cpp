@@ -105,15 +105,16 @@ Geo geo_g(const fs_slice_params* p, int dk) {
 // 8-wave block per CU (86 KB of LDS, two waves per SIMD), so the grid targets
 // one block per CU; P = blocks per (b, h), at most the G-blocked slot-owned
 // grid's partitions, whose partial buffer it reuses (one partial per block).
-constexpr int64_t kCoopBlocks = 256;
+// The slice forward (128 registers, 68 KB of LDS) fits two blocks per CU.
+constexpr int64_t kCoopBlocksBwd = 256, kCoopBlocksFwd = 512;
 bool coop_on(const fs_slice_params* p, int mode) {
   return mode == 2 && fs::coop_ok((int)p->G, (int)p->D, (int)p->DV);
 }
-Geo geo_coop(const fs_slice_params* p) {
+Geo geo_coop(const fs_slice_params* p, int64_t target) {
   Geo g;
   g.ntiles = (int)((p->N + fs::kTile - 1) / fs::kTile);
   const int64_t bh = p->B * p->H;
-  int64_t P = (kCoopBlocks + bh - 1) / bh;
+  int64_t P = (target + bh - 1) / bh;
   if (P > g.ntiles) P = g.ntiles;
   if (P < 1) P = 1;
   const int64_t cap = geo_g(p, -1).P;
@@ -493,7 +494,7 @@ int32_t slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_params
     rc = hip_check(fs::launch_fused_slice_fwd(a, x->dtype, mode, st), who);
   } else if (coop_on(p, mode)) {
     // one pass: the statistics from stats_in, or formed in the pass
-    g = geo_coop(p);
+    g = geo_coop(p, kCoopBlocksFwd);
     fs::Args a = base_args(p, g);
     set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
     set_in(p, fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
@@ -713,7 +714,7 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
     a.stats_in = stats;
     if (coop) {
       // one pass from the statistics: dfx, dx, and dW, db, dtau per block
-      const Geo gc = geo_coop(p);
+      const Geo gc = geo_coop(p, kCoopBlocksBwd);
       a.P = gc.P;
       a.part = ws.part;
       rc = hip_check(fs::launch_coop(fs::CK_SLICE_BWD, a, x->dtype, st), who);
@@ -810,7 +811,7 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
     a.stats_in = stats;
     if (coop) {
       // one pass from the statistics: dx, and dtokens, dW, db, dtau per block
-      const Geo gc = geo_coop(p);
+      const Geo gc = geo_coop(p, kCoopBlocksBwd);
       a.P = gc.P;
       a.part = ws.part;
       rc = hip_check(fs::launch_coop(fs::CK_DESLICE_BWD, a, x->dtype, st), who);

@@ -47,7 +47,11 @@ constexpr int kCoopPts = 4 * kCoopWaves * 32;    // per-point exchange: 2 buffer
 constexpr int kCoopVec = 2 * 32 * kCoopWaves;    // per-slot vectors: bias * cst, d s
 constexpr int kCoopTileB = kTrPieceB;            // one staged 32 x 32 bf16 tile (bytes)
 constexpr int kCoopTiles = 3 * 2 * kCoopTileB / 4;  // 3 buffers x (x, fx / d_out) (floats)
-constexpr int kCoopLds = kCoopWaves * kCoopWReg + kCoopPts + kCoopVec + kCoopTiles;
+// the slice forward's wave region: the staging of W, then the transpose
+// region and the point-sum buffer of coop_point_sum (no exchange fragments):
+// 68 KB per block, so two blocks share a CU
+constexpr int kCoopWRegFwd = kCoopTr + 17 * 64;
+static_assert(32 * kCoopStride <= kCoopWRegFwd, "coop forward staging exceeds its region");
 
 // the shapes these kernels serve (the host picks them for dot kind 2)
 __host__ __device__ inline bool coop_serves(int G, int D, int DV) {
@@ -80,8 +84,10 @@ __device__ __forceinline__ float coop_point_sum(const float (&v)[16], float* reg
   return s;
 }
 
-#define COOP_PROLOGUE                                                                   \
-  __shared__ __attribute__((aligned(16))) float smem[kCoopLds];                         \
+#define COOP_PROLOGUE(WREG)                                                             \
+  constexpr int kWReg_ = (WREG);                                                        \
+  __shared__ __attribute__((aligned(16))) float smem[kCoopWaves * kWReg_ + kCoopPts +    \
+                                                     kCoopVec + kCoopTiles];            \
   constexpr int M = MMA_BF16;                                                           \
   const int lane = threadIdx.x & 63;                                                    \
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);                     \
@@ -94,9 +100,9 @@ __device__ __forceinline__ float coop_point_sum(const float (&v)[16], float* reg
   const int G = a.G, D = a.D, DV = a.DV;                                                \
   const int g0 = 32 * wid;                                                              \
   const int pid = blockIdx.x;                                                           \
-  float* wreg = smem + wid * kCoopWReg;                                                 \
+  float* wreg = smem + wid * kWReg_;                                                    \
   char* trS = reinterpret_cast<char*>(wreg);                                            \
-  float* xpt = smem + kCoopWaves * kCoopWReg;                                           \
+  float* xpt = smem + kCoopWaves * kWReg_;                                              \
   float* sBC = xpt + kCoopPts;                                                          \
   float* sDS = sBC + 32 * kCoopWaves;                                                   \
   char* tiles_ = reinterpret_cast<char*>(sDS + 32 * kCoopWaves);                        \
@@ -108,7 +114,7 @@ __device__ __forceinline__ float coop_point_sum(const float (&v)[16], float* reg
   const float* Bp = a.bias + b * a.sbb + hd * a.sbh;                                    \
   const int Rw = G - g0 < 32 ? G - g0 : 32;                                             \
   coop_stage(wreg, Wp + (int64_t)g0 * D, Rw, D, lane);                                  \
-  if (a.tok)                                                                            \
+  if (a.tok && kWReg_ >= 2 * 32 * kCoopStride)                                          \
     coop_stage(wreg + 32 * kCoopStride, a.tok + ((int64_t)bh * G + g0) * DV, Rw, DV, lane); \
   if (lane < 32) {                                                                      \
     const int g = g0 + lane;                                                            \
@@ -210,8 +216,8 @@ __device__ __forceinline__ void tile_rows(Frag<MMA_BF16>& f, const char* region,
 // pair while another still reads this one's) and written to stats_out when
 // asked for.
 template <typename T>
-__global__ __launch_bounds__(kCoopThreads, 1) void k_coop_slice_fwd(Args a) {
-  COOP_PROLOGUE
+__global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
+  COOP_PROLOGUE(kCoopWRegFwd)
   __syncthreads();  // the staging area becomes the transpose region
   f32x16 zacc = zero16();
   float sacc[16];
@@ -277,14 +283,15 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_slice_fwd(Args a) {
         w[r] = e[r] * inv;
         sacc[r] += w[r];
       }
-      // z_num += w^T fx: w read back transposed, carrying the tile's sign;
-      // fx^T straight from the staged tile
+      // z_num += w^T fx: w read back transposed, fx^T straight from the
+      // staged tile, chained through the accumulator (the sign alternation
+      // of the fp32-accurate kernels, acc_add, is below bf16's resolution)
       Frag<M> wq, wTq, fT;
       prep<M>(wq, w);
-      tr_put<M>(trS, wq, c, h, sg < 0.f ? 0x80008000u : 0u);
+      tr_put<M>(trS, wq, c, h, 0u);
       tr_get<M>(wTq, trS, lane);
       tr_get<M>(fT, tile_at(cur, 1), lane);
-      mma_acc<M>(zacc, fT, wTq, sg);
+      zacc = mma<M>(fT, wTq, zacc);
     };
     int t = pid, cur = 0;
     gload(t);
@@ -325,7 +332,7 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_slice_fwd(Args a) {
 // row terms of the wave's slots.
 template <typename T, bool SLICE>
 __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
-  COOP_PROLOGUE
+  COOP_PROLOGUE(kCoopWReg)
   Frag<M> qVr, qVc, qWc;  // V [g, v] (omega), V [v, g] (dfx), W / tau [d, g] (dx)
   {
     float f_[16];
@@ -360,18 +367,26 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
   auto run = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
     COOP_STAGING(FAST)
+    // the statistics of a wave's tiles, loaded one tile ahead (a load waited
+    // for in the same tile would expose a whole memory latency per tile);
+    // [parity]: the even / odd bodies of the unrolled loop
+    float smv[2], slv[2];
+    auto sload = [&](int t, int q) {
+      smv[q] = ld_pt(pts_rsrc(sm, (int64_t)t * kTile, N), c);
+      slv[q] = ld_pt(pts_rsrc(sl, (int64_t)t * kTile, N), c);
+    };
     auto body = [&](int t, int cur, auto par) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
-      constexpr float sg = decltype(par)::sign;
-      constexpr uint32_t neg = sg < 0.f ? 0x80008000u : 0u;
+      constexpr int q = decltype(par)::sign < 0.f ? 1 : 0;
       Frag<M> xq, fq;
       tile_rows(xq, tile_at(cur, 0), c, h);
       tile_rows(fq, tile_at(cur, 1), c, h);
       float t2[16];
       COOP_LOGITS(t2, xq)
-      const float m2 = ld_pt(pts_rsrc(sm, p0, N), c) * kLog2e;
-      const float l = ld_pt(pts_rsrc(sl, p0, N), c);
+      const float m2 = smv[q] * kLog2e;
+      const float l = slv[q];
+      sload(t + a.P, q ^ 1);
       const float inv = pv ? 1.f / l : 0.f;
       float w[16], om[16];
       {
@@ -396,9 +411,9 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
         // read back transposed
         Frag<M> oTq, wTq;
         tr_get<M>(oTq, tile_at(cur, 1), lane);
-        tr_put<M>(trS, wq, c, h, neg);
+        tr_put<M>(trS, wq, c, h, 0u);
         tr_get<M>(wTq, trS, lane);
-        mma_acc<M>(dT, oTq, wTq, sg);
+        dT = mma<M>(oTq, wTq, dT);
       }
       lstore(cur == 2 ? 0 : cur + 1);  // publish the next tile
       __syncthreads();
@@ -433,10 +448,10 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
       // transposed
       {
         Frag<M> xTq, lTq;
-        tr_put<M>(trS, lq, c, h, neg);
+        tr_put<M>(trS, lq, c, h, 0u);
         tr_get<M>(lTq, trS, lane);
         tr_get<M>(xTq, tile_at(cur, 0), lane);
-        mma_acc<M>(dW, xTq, lTq, sg);
+        dW = mma<M>(xTq, lTq, dW);
       }
       __syncthreads();
       // sum the eight waves' partials of this wave's two registers, fixed order
@@ -446,7 +461,7 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
         const int j = j0 + q;
         float s = 0.f;
 #pragma unroll
-        for (int wv = 0; wv < kCoopWaves; ++wv) s += smem[wv * kCoopWReg + kCoopTr + j * 64 + lane];
+        for (int wv = 0; wv < kCoopWaves; ++wv) s += smem[wv * kWReg_ + kCoopTr + j * 64 + lane];
         Buf<T>::st1(rdx, vcx + (uint32_t)tile_row(j) * (uint32_t)dx_sn, s);
       }
       if (SLICE) {
@@ -457,7 +472,7 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
           float s = 0.f;
 #pragma unroll
           for (int wv = 0; wv < kCoopWaves; ++wv)
-            s += smem[wv * kCoopWReg + kCoopTr + kCoopX + j * 64 + lane];
+            s += smem[wv * kWReg_ + kCoopTr + kCoopX + j * 64 + lane];
           Buf<T>::st1(rdf, vcf + (uint32_t)tile_row(j) * (uint32_t)df_sn, s);
         }
       }
@@ -466,6 +481,7 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
     gload(t);
     lstore(0);
     gload(t + a.P);
+    sload(t, 0);
     __syncthreads();
     while (t < ntiles_) {
       body(t, cur, TileEven());
