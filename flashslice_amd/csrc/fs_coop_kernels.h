@@ -34,6 +34,9 @@
 namespace fs {
 
 constexpr int kCoopWaves = 8;
+// the exponent shift of points beyond N: every weight exp2(t2 - shift) is 0
+// and every product with the shifted logit stays finite
+constexpr float kFarShift = 3.0e38f;
 constexpr int kCoopThreads = 64 * kCoopWaves;
 constexpr int kCoopStride = 36;                  // staging row stride (floats), conflict-free
 constexpr int kCoopTr = kTrPieceB / 4;           // the wave's transpose region (floats)
@@ -95,8 +98,9 @@ __device__ __forceinline__ float coop_point_sum(const float (&v)[16], float* reg
   const int bh = blockIdx.y;                                                            \
   const int b = bh / a.H, hd = bh - b * a.H;                                            \
   const Rows R_ = rows_of(a, b, hd);                                                    \
-  const int64_t row0_ = R_.row0;                                                        \
-  const int N = R_.N, ntiles_ = R_.ntiles;                                              \
+  const int64_t row0_ = uniform64(R_.row0);                                             \
+  const int N = __builtin_amdgcn_readfirstlane(R_.N);                                   \
+  const int ntiles_ = __builtin_amdgcn_readfirstlane(R_.ntiles);                        \
   const int G = a.G, D = a.D, DV = a.DV;                                                \
   const int g0 = 32 * wid;                                                              \
   const int pid = blockIdx.x;                                                           \
@@ -192,14 +196,19 @@ __device__ __forceinline__ void tile_rows(Frag<MMA_BF16>& f, const char* region,
 // second stream (fx or d_out); three LDS buffers rotate, so the tile stored
 // for the next step never overwrites one a slower wave may still read.
 #define COOP_STAGING(FAST)                                                              \
-  const int tid_ = threadIdx.x, li_ = tid_ & 127;                                       \
-  const bool ldx_ = tid_ < 128, ldf_ = tid_ >= 128 && tid_ < 256;                       \
+  /* waves 0, 1 load x, waves 2, 3 the second stream: conditions on the   */           \
+  /* (scalar) wave index, so each load sees one uniform buffer resource   */           \
+  const int li_ = ((wid & 1) << 6) | lane;                                              \
+  const bool ldx_ = wid < 2, ldf_ = wid >= 2 && wid < 4;                                \
   uint32_t stg_[4] = {0u, 0u, 0u, 0u};                                                  \
-  auto gload = [&](int t) {                                                             \
-    const int64_t p0 = (int64_t)t * kTile;                                              \
-    if (ldx_) coop_tile_load<T, FAST>(stg_, rows_rsrc(x_b, x_sn, x_w, p0, N), x_sn, D, li_); \
-    else if (ldf_)                                                                      \
-      coop_tile_load<T, FAST>(stg_, rows_rsrc(f_b, f_sn, f_w, p0, N), f_sn, DV, li_);   \
+  /* the block's tiles in order: pid, pid + P, ... (one cursor per wave) */             \
+  TileCursor gk_ = ldx_ ? tile_cursor(x_b, x_sn, x_w, pid, a.P, N)                      \
+                        : tile_cursor(f_b, f_sn, f_w, pid, a.P, N);                     \
+  const int64_t gsn_ = ldx_ ? x_sn : f_sn;                                              \
+  const int gC_ = ldx_ ? D : DV;                                                        \
+  auto gload = [&]() {                                                                  \
+    if (ldx_ || ldf_) coop_tile_load<T, FAST>(stg_, gk_.rsrc(), gsn_, gC_, li_);        \
+    gk_.next();                                                                         \
   };                                                                                    \
   auto tile_at = [&](int buf, int stream) -> char* {                                    \
     return tiles_ + (2 * buf + stream) * kCoopTileB;                                    \
@@ -232,9 +241,11 @@ __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
   auto run = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
     COOP_STAGING(FAST)
+    // per-point statistics of the block's tiles, in order (read or written)
+    TileCursor km = tile_cursor(sm ? sm : st_m, 4, 4, pid, a.P, (sm || st_m) ? N : 0);
+    TileCursor kl = tile_cursor(sm ? sm + R_.NS : st_l, 4, 4, pid, a.P, (sm || st_m) ? N : 0);
     auto body = [&](int t, int cur, auto par) {
-      const int64_t p0 = (int64_t)t * kTile;
-      const bool pv = p0 + c < N;
+      const bool pv = t * kTile + c < N;
       constexpr float sg = decltype(par)::sign;
       Frag<M> xq;
       tile_rows(xq, tile_at(cur, 0), c, h);
@@ -260,11 +271,11 @@ __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
       }
       lstore(cur == 2 ? 0 : cur + 1);  // publish the next tile
       __syncthreads();
-      gload(t + 2 * a.P);  // the tile after it, into the staging registers
+      gload();  // the tile after it (t + 2 P), into the staging registers
       float m2, l;
       if (sm) {
-        m2 = ld_pt(pts_rsrc(sm, p0, N), c) * kLog2e;
-        l = ld_pt(pts_rsrc(sm + R_.NS, p0, N), c);
+        m2 = ld_pt(km.rsrc(), c) * kLog2e;
+        l = ld_pt(kl.rsrc(), c);
       } else {
         m2 = xb[c];
 #pragma unroll
@@ -273,10 +284,12 @@ __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
 #pragma unroll
         for (int w = 0; w < kCoopWaves; ++w)
           l += xb[kCoopWaves * 32 + w * 32 + c] * __builtin_amdgcn_exp2f(xb[w * 32 + c] - m2);
-        if (wid == 0) store_stats_tile(st_m, st_l, p0, N, c, h, m2, l);
+        if (wid == 0 && st_m) store_stats_at(km.rsrc(), kl.rsrc(), c, h, m2, l);
       }
+      km.next();
+      kl.next();
       // w = exp2(t2 - m) exp2(m - m2) / l
-      const float inv = pv ? __builtin_amdgcn_exp2f(m - m2) / l : 0.f;
+      const float inv = pv ? __builtin_amdgcn_exp2f(m - m2) * __builtin_amdgcn_rcpf(l) : 0.f;
       float w[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -294,9 +307,9 @@ __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
       zacc = mma<M>(fT, wTq, zacc);
     };
     int t = pid, cur = 0;
-    gload(t);
+    gload();  // t
     lstore(0);
-    gload(t + a.P);
+    gload();  // t + P
     __syncthreads();
     while (t < ntiles_) {
       body(t, cur, TileEven());
@@ -346,6 +359,13 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
     prep<M>(qWc, f_);
   }
   (void)qVc;
+  f32x16 dsC = zero16();  // d s of the wave's slots, per register (slice)
+  if (SLICE) {
+    float dsv[16];
+    lds_frag_vec(dsv, sDS + g0, h);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dsC[r] = dsv[r];
+  }
   __syncthreads();  // the staging area becomes the transpose and exchange regions
   f32x16 dW = zero16(), dT = zero16();
   float dbacc[16], dtacc = 0.f;
@@ -371,34 +391,41 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
     // for in the same tile would expose a whole memory latency per tile);
     // [parity]: the even / odd bodies of the unrolled loop
     float smv[2], slv[2];
-    auto sload = [&](int t, int q) {
-      smv[q] = ld_pt(pts_rsrc(sm, (int64_t)t * kTile, N), c);
-      slv[q] = ld_pt(pts_rsrc(sl, (int64_t)t * kTile, N), c);
+    TileCursor km = tile_cursor(sm, 4, 4, pid, a.P, N), kl = tile_cursor(sl, 4, 4, pid, a.P, N);
+    auto sload = [&](int q) {
+      smv[q] = ld_pt(km.rsrc(), c);
+      slv[q] = ld_pt(kl.rsrc(), c);
+      km.next();
+      kl.next();
     };
+    TileCursor kdx = tile_cursor(dx_b, dx_sn, dx_w, pid, a.P, N);
+    TileCursor kdf = tile_cursor(df_b, df_sn, df_w, pid, a.P, N);
+    (void)kdf;
     auto body = [&](int t, int cur, auto par) {
-      const int64_t p0 = (int64_t)t * kTile;
-      const bool pv = p0 + c < N;
+      const bool pv = t * kTile + c < N;
       constexpr int q = decltype(par)::sign < 0.f ? 1 : 0;
       Frag<M> xq, fq;
       tile_rows(xq, tile_at(cur, 0), c, h);
       tile_rows(fq, tile_at(cur, 1), c, h);
       float t2[16];
       COOP_LOGITS(t2, xq)
-      const float m2 = smv[q] * kLog2e;
-      const float l = slv[q];
-      sload(t + a.P, q ^ 1);
-      const float inv = pv ? 1.f / l : 0.f;
+      // w = exp2(t2 - m2) / l = exp2(t2 - sh) with sh = m2 + log2 l (the
+      // saved l >= 1); points beyond N get sh = kFarShift, hence w = 0. The
+      // row term below uses t2 - sh: shifting a point's logits by a constant
+      // leaves sum_g Lb t2 unchanged, since sum_g Lb = 0.
+      const float sh = pv ? fmaf(smv[q], kLog2e, __builtin_amdgcn_logf(slv[q])) : kFarShift;
+      sload(q ^ 1);  // t + P
       float w[16], om[16];
       {
-        const f32x16 o = mma<M>(qVr, fq, zero16());
-        float dsv[16];
-        if (SLICE) lds_frag_vec(dsv, sDS + g0, h);
+        // omega = V x (+ d s, the slice backward's per-slot term, as the
+        // accumulator's initial value)
+        const f32x16 o = mma<M>(qVr, fq, dsC);
         float d = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          t2[r] -= m2;
-          w[r] = __builtin_amdgcn_exp2f(t2[r]) * inv;
-          om[r] = SLICE ? o[r] + dsv[r] : o[r];
+          t2[r] -= sh;
+          w[r] = __builtin_amdgcn_exp2f(t2[r]);
+          om[r] = o[r];
           d += w[r] * om[r];
         }
         d = pair_sum(d);
@@ -417,7 +444,7 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
       }
       lstore(cur == 2 ? 0 : cur + 1);  // publish the next tile
       __syncthreads();
-      gload(t + 2 * a.P);
+      gload();  // t + 2 P
       float delta = 0.f;
 #pragma unroll
       for (int wv = 0; wv < kCoopWaves; ++wv) delta += xpt[wv * 32 + c];
@@ -455,7 +482,8 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
       }
       __syncthreads();
       // sum the eight waves' partials of this wave's two registers, fixed order
-      const Rsrc rdx = rows_rsrc(dx_b, dx_sn, dx_w, p0, N);
+      const Rsrc rdx = kdx.rsrc();
+      kdx.next();
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int j = j0 + q;
@@ -465,7 +493,8 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
         Buf<T>::st1(rdx, vcx + (uint32_t)tile_row(j) * (uint32_t)dx_sn, s);
       }
       if (SLICE) {
-        const Rsrc rdf = rows_rsrc(df_b, df_sn, df_w, p0, N);
+        const Rsrc rdf = kdf.rsrc();
+        kdf.next();
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           const int j = j0 + q;
@@ -478,10 +507,10 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
       }
     };
     int t = pid, cur = 0;
-    gload(t);
+    gload();  // t
     lstore(0);
-    gload(t + a.P);
-    sload(t, 0);
+    gload();  // t + P
+    sload(0);  // t
     __syncthreads();
     while (t < ntiles_) {
       body(t, cur, TileEven());

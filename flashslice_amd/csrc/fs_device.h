@@ -70,6 +70,16 @@ __device__ __forceinline__ f32x16 mma32(const float (&a)[16], const float (&b)[1
   return c;
 }
 
+
+// A value the wave holds in every lane alike, moved to scalar registers (the
+// compiler cannot always prove it uniform, e.g. after a load through a
+// vector register).
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 // Accumulators that run over a wave's whole stream of point tiles (z_num,
 // dtokens, dW) are kept free of the bf16 MFMA's rounding bias. On MI355X the
 // MFMA sums its products with a small downward bias when they span many

@@ -57,6 +57,42 @@ __device__ __forceinline__ Rsrc rows_rsrc_sel(const void* base, int64_t snb, int
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(p), (short)0, (int)rem, kRsrcWord3);
 }
 
+// The tiles a wave visits in a fixed sequence (first, first + P, ...) of one
+// stream: a cursor holds the current tile's first row and the rows from it
+// to N, and forms the tile's resource with 32-bit arithmetic (the range
+// covers at most the tile's 32 rows, below 2^31 bytes by the host's check of
+// 32 x row stride) instead of the 64-bit multiply of rows_rsrc per tile. The
+// resources equal rows_rsrc's wherever the tile's accesses fall.
+struct TileCursor {
+  const char* p;  // the current tile's first row
+  int64_t step;   // bytes from one tile of the sequence to the next
+  int left;       // rows from the current tile's first row to N (<= 0: none)
+  int pstep;      // rows from one tile of the sequence to the next
+  int snb, rowb;  // row stride and row width in bytes
+  __device__ __forceinline__ Rsrc rsrc() const {
+    const int rows = left < 32 ? left : 32;
+    const int rem = rows > 0 ? (rows - 1) * snb + rowb : 0;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(p), (short)0, rem, kRsrcWord3);
+  }
+  __device__ __forceinline__ void next() {
+    p += step;
+    left -= pstep;
+  }
+};
+// A cursor at tile t0 of a slice (byte base of row 0, row stride snb, row
+// width rowb bytes) that advances by P tiles of 32 rows.
+__device__ __forceinline__ TileCursor tile_cursor(const void* base, int64_t snb, int64_t rowb,
+                                                  int t0, int P, int N) {
+  TileCursor k;
+  k.p = (const char*)base + (int64_t)t0 * 32 * snb;
+  k.step = (int64_t)P * 32 * snb;
+  k.left = N - 32 * t0;
+  k.pstep = 32 * P;
+  k.snb = (int)snb;
+  k.rowb = (int)rowb;
+  return k;
+}
+
 // Typed single-element and four-element accesses (fp32 compute values).
 template <typename T> struct Buf;
 template <> struct Buf<float> {

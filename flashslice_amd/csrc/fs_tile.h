@@ -128,12 +128,15 @@ __device__ __forceinline__ float jacobian_tile(float (&om)[NGB][16], const float
 // store_stats for the tile loops that address points through buffer
 // resources: `sm` / `sl` are the max and sum rows of this (b, h) (null: no
 // statistics); points beyond N and lanes h = 1 store nothing.
+__device__ __forceinline__ void store_stats_at(Rsrc rm, Rsrc rl, int c, int h, float m2, float l,
+                                               bool l_roundtrip = false) {
+  st_pt(rm, c, h, m2 * kLn2);
+  st_pt(rl, c, h, l_roundtrip ? l : l * __builtin_amdgcn_exp2f(m2 - stats_max_roundtrip(m2)));
+}
 __device__ __forceinline__ void store_stats_tile(const float* sm, const float* sl, int64_t p0,
                                                  int N, int c, int h, float m2, float l,
                                                  bool l_roundtrip = false) {
-  st_pt(pts_rsrc(sm, p0, N), c, h, m2 * kLn2);
-  st_pt(pts_rsrc(sl, p0, N), c, h,
-        l_roundtrip ? l : l * __builtin_amdgcn_exp2f(m2 - stats_max_roundtrip(m2)));
+  store_stats_at(pts_rsrc(sm, p0, N), pts_rsrc(sl, p0, N), c, h, m2, l, l_roundtrip);
 }
 
 // A 32-point tile's [point-outer, column-inner] fragments of one (B, N, H, C)
