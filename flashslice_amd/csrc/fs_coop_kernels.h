@@ -40,12 +40,17 @@ constexpr float kFarShift = 3.0e38f;
 constexpr int kCoopThreads = 64 * kCoopWaves;
 constexpr int kCoopStride = 36;                  // staging row stride (floats), conflict-free
 constexpr int kCoopTr = kTrPieceB / 4;           // the wave's transpose region (floats)
-constexpr int kCoopX = 16 * 64;                  // one f32x16 per lane (floats)
-// per wave: during the prologue the fp32 staging of its 32 rows of W and of
-// tokens / dz_num; in the tile loop the transpose region and two exchange
-// fragments (dx, dfx)
-constexpr int kCoopWReg = kCoopTr + 2 * kCoopX;
-static_assert(2 * 32 * kCoopStride <= kCoopWReg, "coop staging exceeds the wave region");
+// per wave, during the prologue: the fp32 staging of its 32 rows of W and of
+// tokens / dz_num (the backward) or of W (the slice forward)
+constexpr int kCoopWReg = 2 * 32 * kCoopStride;
+// The backward's tile loop reuses the waves' staging regions: eight
+// transpose regions, then the block's [point][slot] bf16 buffers of Lb and
+// w (32 rows of 256 slots, each row padded by 16 bytes: the 16 lanes that
+// read one 16-byte chunk of 16 rows hit 16 different chunks of the banks)
+constexpr int kPsRowB = 256 * 2 + 16;
+constexpr int kPsBufB = 32 * kPsRowB;
+static_assert(kCoopWaves * kTrPieceB + 2 * kPsBufB <= kCoopWaves * kCoopWReg * 4,
+              "coop backward buffers exceed the staging regions");
 constexpr int kCoopPts = 4 * kCoopWaves * 32;    // per-point exchange: 2 buffers x 2 rows per wave
 constexpr int kCoopVec = 2 * 32 * kCoopWaves;    // per-slot vectors: bias * cst, d s
 constexpr int kCoopTileB = kTrPieceB;            // one staged 32 x 32 bf16 tile (bytes)
@@ -338,27 +343,46 @@ __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
 }
 
 // ---------------------------------------------------------------- backward
+// A [point][slot] bf16 buffer of the block (rows of kPsRowB bytes): lane
+// (c, h) of wave wid writes its fragment f ([point c][slot 32 wid + kmap(j,
+// h)]) as four 8-byte pieces, slots 32 wid + 8 q + 4 h .. + 3.
+__device__ __forceinline__ void ps_put(char* buf, const Frag<MMA_BF16>& f, int wid, int c, int h) {
+  char* row = buf + c * kPsRowB + 8 * h + 64 * wid;
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+      *reinterpret_cast<uint2*>(row + 16 * (2 * s + hh)) =
+          make_uint2(f.q[s][2 * hh], f.q[s][2 * hh + 1]);
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 // One pass of the slice (SLICE) or deslice backward from saved statistics:
 // omega = fx . dz_num + d s (slice) or d_out . tokens (deslice); delta and
 // Lb = w (omega - delta) per point; dx = Lb W / tau and (slice) dfx =
-// w dz_num summed over the waves; dW, db, (deslice) dtokens and the dtau
-// row terms of the wave's slots.
+// w dz_num; dW, db, (deslice) dtokens and the dtau row terms of the wave's
+// slots.
+//
+// dx and dfx contract over all G slots, which the eight waves hold 32 each:
+// every wave writes its Lb (and w) into the block's [point][slot] buffers,
+// and after the tile's second barrier four waves per output each compute a
+// 16-point x 16-column block of it over all slots with
+// v_mfma_f32_16x16x32_bf16 (operand lanes l supply contraction indices
+// 8 (l / 16) .. + 7, the same on both operands; output lane l holds column
+// l % 16 and rows 4 (l / 16) .. + 3): A = (W / tau) [d][g] or dz_num [v][g],
+// held in registers for the whole pass, B = the buffer's [g][p] read in
+// 16-byte rows. The sum over slots is the MFMA's own, in a fixed order, and
+// each lane stores four consecutive columns of one point.
 template <typename T, bool SLICE>
 __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
   COOP_PROLOGUE(kCoopWReg)
-  Frag<M> qVr, qVc, qWc;  // V [g, v] (omega), V [v, g] (dfx), W / tau [d, g] (dx)
+  Frag<M> qVr;  // V [g, v] (omega)
   {
     float f_[16];
     lds_frag_rowouter(f_, wreg + 32 * kCoopStride, kCoopStride, 0, 0, c, h);
     prep<M>(qVr, f_);
-    lds_frag_colouter(f_, wreg + 32 * kCoopStride, kCoopStride, 0, 0, c, h);
-    prep<M>(qVc, f_);
-    lds_frag_colouter(f_, wreg, kCoopStride, 0, 0, c, h);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) f_[j] *= inv_tau;
-    prep<M>(qWc, f_);
   }
-  (void)qVc;
   f32x16 dsC = zero16();  // d s of the wave's slots, per register (slice)
   if (SLICE) {
     float dsv[16];
@@ -366,7 +390,30 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dsC[r] = dsv[r];
   }
-  __syncthreads();  // the staging area becomes the transpose and exchange regions
+  // this wave's output block: stream os (0 dx, 1 dfx), points 16 ph ..,
+  // columns 16 dh ..; its A operand over the 8 slot steps of 32 (slots
+  // 32 ks + 8 kg + e of lane group kg = lane / 16)
+  const int os = SLICE ? wid >> 2 : 0, ph = (wid >> 1) & 1, dh = wid & 1;
+  const bool out_ = SLICE || wid < 4;
+  const int kg = lane >> 4, l16 = lane & 15;
+  bf16x8 Ao[kCoopWaves];
+  {
+    const float* src = os == 0 ? Wp : a.tok + (int64_t)bh * G * DV;
+    const int C = os == 0 ? D : DV, col = 16 * dh + l16;
+    const float sc = os == 0 ? inv_tau : 1.f;
+#pragma unroll
+    for (int ks = 0; ks < kCoopWaves; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int g = 32 * ks + 8 * kg + e;
+        Ao[ks][e] = (__bf16)((out_ && g < G && col < C) ? src[(int64_t)g * C + col] * sc : 0.f);
+      }
+  }
+  __syncthreads();  // the staging regions become the transpose regions and buffers
+  char* trB = reinterpret_cast<char*>(smem) + wid * kTrPieceB;
+  char* lbuf = reinterpret_cast<char*>(smem) + kCoopWaves * kTrPieceB;
+  char* wbuf = lbuf + kPsBufB;
+  const char* obuf = os == 0 ? lbuf : wbuf;  // B operand of this wave's output
   f32x16 dW = zero16(), dT = zero16();
   float dbacc[16], dtacc = 0.f;
 #pragma unroll
@@ -376,14 +423,11 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
   COOP_SLICE(dx, a.o1, a.s1b, a.s1n, a.s1h, D)
   COOP_SLICE(df, a.o2, a.s2b, a.s2n, a.s2h, DV)
   (void)x_row; (void)f_row; (void)dx_row; (void)df_row;
-  const uint32_t vcx = col_off<T>(0, D, dx_sn, c, h);
-  const uint32_t vcf = col_off<T>(0, DV, df_sn, c, h);
-  (void)vcf;
   const float* sm = a.stats_in + R_.stats_off();
   const float* sl = sm + R_.NS;
-  // registers 2 wid, 2 wid + 1 of the exchanged fragments are this wave's to
-  // sum and store (rows 4 h + tile_row(j) of the tile)
-  const int j0 = 2 * wid;
+  // the output block's lane: point 16 ph + l16, columns oc .. oc + 3
+  const int op = 16 * ph + l16, oc = 16 * dh + 4 * kg;
+  const int oC = os == 0 ? D : DV;
   auto run = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
     COOP_STAGING(FAST)
@@ -398,9 +442,10 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
       km.next();
       kl.next();
     };
-    TileCursor kdx = tile_cursor(dx_b, dx_sn, dx_w, pid, a.P, N);
-    TileCursor kdf = tile_cursor(df_b, df_sn, df_w, pid, a.P, N);
-    (void)kdf;
+    TileCursor ko = os == 0 ? tile_cursor(dx_b, dx_sn, dx_w, pid, a.P, N)
+                            : tile_cursor(df_b, df_sn, df_w, pid, a.P, N);
+    const int64_t osn = os == 0 ? dx_sn : df_sn;
+    const uint32_t ooff = (uint32_t)(op * osn) + (uint32_t)(oc * (int)sizeof(T));
     auto body = [&](int t, int cur, auto par) {
       const bool pv = t * kTile + c < N;
       constexpr int q = decltype(par)::sign < 0.f ? 1 : 0;
@@ -438,8 +483,8 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
         // read back transposed
         Frag<M> oTq, wTq;
         tr_get<M>(oTq, tile_at(cur, 1), lane);
-        tr_put<M>(trS, wq, c, h, 0u);
-        tr_get<M>(wTq, trS, lane);
+        tr_put<M>(trB, wq, c, h, 0u);
+        tr_get<M>(wTq, trB, lane);
         dT = mma<M>(oTq, wTq, dT);
       }
       lstore(cur == 2 ? 0 : cur + 1);  // publish the next tile
@@ -460,49 +505,36 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
       dtacc += (pv && h == 0) ? rt : 0.f;
       Frag<M> lq;
       prep<M>(lq, om);
-      // this wave's partials of dx (and dfx) for the exchange
-      {
-        const f32x16 px = mma<M>(lq, qWc, zero16());
-#pragma unroll
-        for (int r = 0; r < 16; ++r) wreg[kCoopTr + r * 64 + lane] = px[r];
-        if (SLICE) {
-          const f32x16 pf = mma<M>(wq, qVc, zero16());
-#pragma unroll
-          for (int r = 0; r < 16; ++r) wreg[kCoopTr + kCoopX + r * 64 + lane] = pf[r];
-        }
-      }
+      // Lb (and w) into the block's buffers for the dx (dfx) contraction
+      ps_put(lbuf, lq, wid, c, h);
+      if (SLICE) ps_put(wbuf, wq, wid, c, h);
       // dW += x^T Lb: x^T straight from the staged tile, Lb read back
       // transposed
       {
         Frag<M> xTq, lTq;
-        tr_put<M>(trS, lq, c, h, 0u);
-        tr_get<M>(lTq, trS, lane);
+        tr_put<M>(trB, lq, c, h, 0u);
+        tr_get<M>(lTq, trB, lane);
         tr_get<M>(xTq, tile_at(cur, 0), lane);
         dW = mma<M>(xTq, lTq, dW);
       }
       __syncthreads();
-      // sum the eight waves' partials of this wave's two registers, fixed order
-      const Rsrc rdx = kdx.rsrc();
-      kdx.next();
+      // this wave's 16 x 16 block of dx (dfx) over all slots
+      const Rsrc ro = ko.rsrc();
+      ko.next();
+      if (out_) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const char* brow = obuf + op * kPsRowB + 16 * kg;
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int j = j0 + q;
-        float s = 0.f;
+        for (int ks = 0; ks < kCoopWaves; ++ks) {
+          const bf16x8 bv = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(brow + 64 * ks));
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ao[ks], bv, acc, 0, 0, 0);
+        }
+        if (FAST) {
+          Buf<T>::st4(ro, ooff, acc[0], acc[1], acc[2], acc[3]);
+        } else {
 #pragma unroll
-        for (int wv = 0; wv < kCoopWaves; ++wv) s += smem[wv * kWReg_ + kCoopTr + j * 64 + lane];
-        Buf<T>::st1(rdx, vcx + (uint32_t)tile_row(j) * (uint32_t)dx_sn, s);
-      }
-      if (SLICE) {
-        const Rsrc rdf = kdf.rsrc();
-        kdf.next();
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const int j = j0 + q;
-          float s = 0.f;
-#pragma unroll
-          for (int wv = 0; wv < kCoopWaves; ++wv)
-            s += smem[wv * kWReg_ + kCoopTr + kCoopX + j * 64 + lane];
-          Buf<T>::st1(rdf, vcf + (uint32_t)tile_row(j) * (uint32_t)df_sn, s);
+          for (int r = 0; r < 4; ++r)
+            Buf<T>::st1(ro, oc + r < oC ? ooff + (uint32_t)(r * (int)sizeof(T)) : kOff, acc[r]);
         }
       }
     };

@@ -126,6 +126,14 @@ template <> struct Buf<__bf16> {
     const __bf16 b = (__bf16)v;
     __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, b), r, off, 0, kStream);
   }
+  // four consecutive elements, one 8-byte store (off 8-byte aligned)
+  static __device__ __forceinline__ void st4(Rsrc r, uint32_t off, float v0, float v1, float v2,
+                                             float v3) {
+    typedef __bf16 b4 __attribute__((ext_vector_type(4)));
+    const b4 b = {(__bf16)v0, (__bf16)v1, (__bf16)v2, (__bf16)v3};
+    typedef unsigned u2 __attribute__((ext_vector_type(2)));
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, b), r, off, 0, kStream);
+  }
 };
 template <> struct Buf<_Float16> {
   static __device__ __forceinline__ float h2f(uint32_t b16) {
@@ -144,6 +152,13 @@ template <> struct Buf<_Float16> {
   static __device__ __forceinline__ void st1(Rsrc r, uint32_t off, float v) {
     const _Float16 b = (_Float16)v;
     __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, b), r, off, 0, kStream);
+  }
+  static __device__ __forceinline__ void st4(Rsrc r, uint32_t off, float v0, float v1, float v2,
+                                             float v3) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 b = {(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3};
+    typedef unsigned u2 __attribute__((ext_vector_type(2)));
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, b), r, off, 0, kStream);
   }
 };
 
