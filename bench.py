@@ -30,6 +30,11 @@ four ops' algorithmic bytes over the step), ``cpu_baseline`` (the CPU
 oracle -- the eager PyTorch softmax/einsum path -- timed on a bounded sample
 on this host's cores), ``peak_hbm_gb``, ``per_op_ms`` and
 ``deterministic``.
+
+``--tied`` times the step with the backward ``fused_coupling`` runs: the
+same gradients through the tied kernel (slice-first: the deslice's dtokens
+pass first, since the token step needs dtokens before the slice's backward;
+then one pass for everything else), its ops in ``per_op_ms``.
 """
 
 import argparse
@@ -130,8 +135,9 @@ def alg_bytes(B, N, H, D, DV, e=4):
     pts = B * N * H
     return {"slice_fwd": pts * (D + DV) * e, "deslice_fwd": pts * (D + DV) * e,
             "deslice_bwd": pts * (2 * D + DV) * e, "slice_bwd": pts * (2 * D + 2 * DV) * e,
-            # the tied backward (--tied): reads x, fx, d_out, writes dx, dfx
-            "tied_bwd": pts * (2 * D + 3 * DV) * e}
+            # the tied backward (--tied): reads x, fx, d_out, writes dx, dfx;
+            # slice-first, the dtokens pass before it reads x, d_out
+            "tied_bwd": pts * (2 * D + 3 * DV) * e, "dtok_pass": pts * (D + DV) * e}
 
 
 def alg_flops(B, N, H, D, DV, G):
@@ -141,8 +147,10 @@ def alg_flops(B, N, H, D, DV, G):
     return {"slice_fwd": u * (D + DV), "deslice_fwd": u * (D + DV),
             "deslice_bwd": u * (3 * D + 2 * DV),  # logits, dtokens, omega, dx, dW
             "slice_bwd": u * (3 * D + 2 * DV),
-            # logits, omega (two value dots), dfx, dtokens, dx, dW
-            "tied_bwd": u * (3 * D + 4 * DV)}
+            # logits, omega (two value dots), dfx, dtokens, dx, dW (slice-first
+            # the dtokens dot is the dtokens pass's: logits and w^T d_out)
+            "tied_bwd": u * (3 * D + 4 * DV), "tied_bwd_sf": u * (3 * D + 3 * DV),
+            "dtok_pass": u * (D + DV)}
 
 
 def measured_traffic(workload):
@@ -183,10 +191,15 @@ def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", dot=0
     given tokens are deslided, then the points are slided again (config 4's
     persistent point stream), and the backward runs in autograd's order
     (slice, then deslice). ``ev``: a (start, end) event pair per op name,
-    recorded around exactly that op. ``tied`` (deslice-first only): the
-    backward is the one tied operator (flashslice::deslice_slice_bwd, one
-    pass for both ops' gradients and a single dx) instead of the two
-    backward ops, whose two dx autograd would still have to add."""
+    recorded around exactly that op. ``tied``: the backward as
+    ``fused_coupling`` runs it instead of the two backward ops (whose two dx
+    autograd would still have to add): deslice-first the one tied operator
+    (flashslice::deslice_slice_bwd, one pass for both ops' gradients and a
+    single dx); slice-first the deslice's dtokens (w^T d_out, a slice pass
+    over x and d_out with the saved statistics: the token step needs them
+    before the slice's backward can start), then one tied pass
+    (flashslice::tied_slice_bwd) for everything else. The forward ops carry
+    the slice's statistics to the deslice and the backward."""
     ops = torch.ops.flashslice
 
     def timed(name, fn, *args):
@@ -218,6 +231,17 @@ def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", dot=0
         dx2, dfx, dW2, db2, dt2 = timed("slice_bwd", slice_b, st, dzb, dsb)
         dx1, dtok, dW1, db1, dt1 = timed("deslice_bwd", deslice_b, tok0, st)
         return z, s, out, dx1, dtok, dW1, db1, dt1, dx2, dfx, dW2, db2, dt2
+    if tied:
+        z, s, st = timed("slice_fwd", ops.slice_blk, x, fx, W, b, tau, None, dot)
+        den = (s + EPS)[..., None]
+        tok = z / den
+        out, _ = timed("deslice_fwd", ops.deslice_blk, x, W, b, tau, tok, st, dot)
+        dtok, _, _ = timed("dtok_pass", ops.slice_blk, x, d_out, W, b, tau, st, dot)
+        dz = dzb + dtok / den
+        ds = dsb - (dtok * tok).sum(-1) / den[..., 0]
+        dx, dfx, dW, db, dt = timed("tied_bwd", ops.tied_slice_bwd, x, fx, W, b, tau, st, dz,
+                                    ds, d_out, tok, dot)
+        return z, s, out, dx, dtok, dW, db, dt, dfx
     z, s, st = timed("slice_fwd", slice_f, None)
     den = (s + EPS)[..., None]
     tok = z / den
@@ -677,8 +701,9 @@ def main():
     ap.add_argument("--dot", default="ieee", choices=sorted(DOTS),
                     help="dot level: ieee (fp32 inputs) or bf16 (x_mid, fx_mid, W in bf16)")
     ap.add_argument("--tied", action="store_true",
-                    help="deslice-first workloads: the backward as the tied operator "
-                         "(fused_deslice_slice's single pass) instead of the two backward ops")
+                    help="the backward as fused_coupling runs it instead of the two backward "
+                         "ops: deslice-first one tied pass; slice-first the dtokens pass, then "
+                         "one tied pass")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="before the warmup, copy x once (B*N*H*D*4 bytes read and written): "
@@ -708,6 +733,8 @@ def main():
         torch.cuda.set_device(0)
         return bench_ragged(a, RAGGED_WORKLOADS[a.workload])
     B, N, H, D, DV, G, layout, order, desc = WORKLOADS[a.workload]
+    if a.dot == "bf16":
+        desc = desc.replace("fp32 ieee", "bf16 inputs and dots")
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     inputs = list(make_inputs(B, N, H, D, DV, G, layout, dev))
@@ -717,10 +744,8 @@ def main():
             inputs[i] = inputs[i].bfloat16()
     from flashslice_amd.kernels.slice_ops import _use_blocked
     blocked = _use_blocked(D, G, DV, dot)
-    if a.tied and order != "deslice-first":
-        print("--tied applies to the deslice-first workloads (c4)", file=sys.stderr)
-        sys.exit(2)
-    ops_timed = (("deslice_fwd", "slice_fwd", "tied_bwd") if a.tied else OPS)
+    ops_timed = ((("deslice_fwd", "slice_fwd", "tied_bwd") if order == "deslice-first" else
+                  ("slice_fwd", "deslice_fwd", "dtok_pass", "tied_bwd")) if a.tied else OPS)
     run_step = functools.partial(step_ops, *inputs, order=order, dot=dot, blocked=blocked,
                                  tied=a.tied)
     torch.cuda.synchronize()
@@ -774,6 +799,8 @@ def main():
     per_op = {n: sum(e[n][0].elapsed_time(e[n][1]) for e in evs) / a.steps for n in ops_timed}
     bytes_ = alg_bytes(B, N, H, D, DV, 2 if a.dot == "bf16" else 4)
     flops = alg_flops(B, N, H, D, DV, G)
+    if order == "slice-first":
+        flops["tied_bwd"] = flops.pop("tied_bwd_sf")
     dom = max(per_op, key=per_op.get)
     ach = bytes_[dom] / (per_op[dom] * 1e-3) / 1e9
     ach_tf = flops[dom] / (per_op[dom] * 1e-3) / 1e12
