@@ -144,9 +144,13 @@ int64_t fused_target(int32_t op, const fs_slice_params* p) {
     // blocks (C2's shape: 1.193 / 1.137 / 1.146 / 1.151 ms at 512 / 1024 /
     // 1536 / 2048)
     case FS_OP_TIED_BWD: t = one ? 1024 : 256; break;
-    // wider shapes: one wave per SIMD, one dispatch round (C4: 0.973 ms
-    // against 0.995 at 512 blocks)
-    case FS_OP_SLICE_FWD: t = one ? 1536 : 256; break;
+    // wider shapes: one dispatch round of the kernel's waves per SIMD (one
+    // wave, 256 blocks; C4 at one wave: 0.973 ms against 0.995 at 512)
+    case FS_OP_SLICE_FWD: {
+      auto b32 = [](int64_t n) { return n <= 32 ? 1 : n <= 64 ? 2 : n <= 128 ? 4 : 8; };
+      t = one ? 1536 : 256 * fs::slice_fwd_waves(b32(p->G), b32(p->D), b32(p->DV));
+      break;
+    }
     // wider shapes: one wave per SIMD and one 100 KB block per CU at C4, one
     // dispatch round (measured at C4: 1.99 ms against 2.13 at 1536 blocks,
     // 2.03 at 512)

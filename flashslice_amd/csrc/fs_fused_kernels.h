@@ -176,9 +176,10 @@ __device__ __forceinline__ void acc_put(float& t, float v, bool first) { t = fir
 // registers, a few values spilled; 5 % faster at C2 with 1536 blocks).
 constexpr int fused_waves(int ngb, int ndb, int nvb) { return ngb * ndb * nvb == 1 ? 2 : 1; }
 
+
 // ------------------------------------------------------------------ slice fwd
 template <typename T, int DK, int NGB, int NDB, int NVB>
-__global__ __launch_bounds__(256, NGB * NDB * NVB == 1 ? 3 : 1) void k_fused_slice_fwd(Args a) {
+__global__ __launch_bounds__(256, slice_fwd_waves(NGB, NDB, NVB)) void k_fused_slice_fwd(Args a) {
   FS_PROLOGUE(NGB, NDB, NVB, 0, kLdsTile)
   FS_PROLOGUE_END
   f32x16 zacc[NGB][NVB];
@@ -268,7 +269,7 @@ __global__ __launch_bounds__(256, NGB * NDB * NVB == 1 ? 3 : 1) void k_fused_sli
     auto load_f = [&](int t) {
       const Rsrc rf = rows_rsrc(f_b, f_sn, f_w, (int64_t)t * kTile, N);
 #pragma unroll
-      for (int vb = 0; vb < NVB; ++vb) ld_cols<T>(fb[vb], rf, vcf[vb], (uint32_t)f_sn);
+      for (int vb = 0; vb < NVB; ++vb) ld_cols_here<T>(fb[vb], rf, vcf[vb], (uint32_t)f_sn);
     };
     auto body = [&](int t, auto par) {
       const int64_t p0 = (int64_t)t * kTile;
@@ -284,28 +285,37 @@ __global__ __launch_bounds__(256, NGB * NDB * NVB == 1 ? 3 : 1) void k_fused_sli
       load_x(t + a.P);
       softmax_tile<NGB>(w, m2, lsum, t2, pv);
       store_stats_tile(st_m, st_l, p0, N, c, h, m2, lsum);
-      Frag<MV> fq[NVB];  // fx carries the tile's sign (acc_add)
-#pragma unroll
-      for (int vb = 0; vb < NVB; ++vb) {
-        float fs[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) fs[j] = fb[vb][j] * sg;
-        prep<MV>(fq[vb], fs);
-      }
-      load_f(t + a.P);
+      // w^T of every slot block as MFMA pieces, then one value block of fx
+      // at a time: the split pieces held are w's for all slot blocks and fx's
+      // for one value block (instead of fx's for all of them next to w in
+      // fp32), which fits two waves per SIMD at config 4's shape
+      Frag<MV> wq[NGB];
 #pragma unroll
       for (int gb = 0; gb < NGB; ++gb) {
         float wT[16];
         transpose32(wT, w[gb], lds, c, h);
-        Frag<MV> wq;
-        prep<MV>(wq, wT);
-#pragma unroll
-        for (int vb = 0; vb < NVB; ++vb) mma_acc<MV>(zacc[gb][vb], fq[vb], wq, sg);
+        prep<MV>(wq[gb], wT);
         float s = 0.f;
 #pragma unroll
         for (int j = 0; j < 16; ++j) s += wT[j];
         sacc[gb] += s;
       }
+#pragma unroll
+      for (int vb = 0; vb < NVB; ++vb) {
+        Frag<MV> fq;  // fx carries the tile's sign (acc_add)
+        {
+          float fs[16];
+#pragma unroll
+          for (int j = 0; j < 16; ++j) fs[j] = fb[vb][j] * sg;
+          prep<MV>(fq, fs);
+        }
+#pragma unroll
+        for (int gb = 0; gb < NGB; ++gb) mma_acc<MV>(zacc[gb][vb], fq, wq[gb], sg);
+        // one value block's products (each a fresh 16-register accumulator,
+        // acc_add) at a time
+        sched_fence();
+      }
+      load_f(t + a.P);
     };
     int t = pid;
     load_x(t);

@@ -169,6 +169,16 @@ int blocked_width_blocks(int D, int DV);  // 1, 2, 4 or 8 (0 if D or DV > 256)
 // whole-G layout (part_floats_*). The backward kernels need statistics.
 enum CoopKind { CK_SLICE_FWD = 0, CK_SLICE_BWD = 1, CK_DESLICE_BWD = 2 };
 hipError_t launch_coop(int kind, const Args& a, int dtype, hipStream_t st);
+
+// Waves per SIMD the whole-G slice forward is compiled for, by its blocks of
+// 32 slots / logits width / value width (the host sizes its grid to fill
+// them): three at one block (168 registers, a few values spilled; 5 % faster
+// at C2 with 1536 blocks); two for a wide shape whose slot accumulators and
+// split pieces fit 256 registers (one block of x, at most two slot blocks,
+// z_num blocks NGB x NVB <= 4); else one.
+__host__ __device__ constexpr int slice_fwd_waves(int ngb, int ndb, int nvb) {
+  return ngb * ndb * nvb == 1 ? 3 : (ndb == 1 && ngb <= 2 && ngb * nvb <= 4 ? 2 : 1);
+}
 bool coop_ok(int G, int D, int DV);
 
 // Deterministic reduction of per-wave partials (fs_reduce.hip). One output

@@ -206,6 +206,16 @@ __device__ __forceinline__ void ld_cols(float (&f)[16], Rsrc r, uint32_t vc, uin
 #pragma unroll
   for (int j = 0; j < 16; ++j) f[j] = Buf<T>::ld1(r, vc + (uint32_t)tile_row(j) * snb);
 }
+// ld_cols whose sixteen row offsets are formed at the call (one add each)
+// rather than hoisted out of the tile loop by the compiler as sixteen
+// loop-invariant registers per call site: for the wide kernels, where those
+// registers would be spilled.
+template <typename T>
+__device__ __forceinline__ void ld_cols_here(float (&f)[16], Rsrc r, uint32_t vc, uint32_t snb) {
+  asm volatile("" : "+v"(vc));
+#pragma unroll
+  for (int j = 0; j < 16; ++j) f[j] = Buf<T>::ld1(r, vc + (uint32_t)tile_row(j) * snb);
+}
 
 // Store a [column-outer, point-inner] fragment (the transposed twin of
 // ld_cols): every store instruction writes two whole 32-column row segments.
