@@ -627,6 +627,20 @@ int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float
     a.stats_out = stats_out;
     return hip_check(fs::launch_fused_deslice_fwd(a, x->dtype, mode, st), who);
   }
+  if (coop_on(p, mode)) {
+    // one pass: the weights of a tile's 256 slots through LDS, out over all
+    // of them on the matrix cores (statistics read or formed in the pass)
+    fs::Args a = base_args(p, geo_coop(p, kCoopBlocksFwd));
+    set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
+    set_out(p, out, &a.o1, &a.s1b, &a.s1n, &a.s1h);
+    a.vec_x = vec_ok(x);
+    a.vec_1 = vec_ok(out);
+    a.fast = a.vec_x && a.vec_1 && full_widths(p);
+    a.tok = tokens;
+    a.stats_in = stats_in;
+    a.stats_out = stats_in ? nullptr : stats_out;
+    return hip_check(fs::launch_coop(fs::CK_DESLICE_FWD, a, x->dtype, st), who);
+  }
   const Geo g = geo_gp(p, GPG_DESLICE, mode);
   fs::Args a = base_args(p, g);
   set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);

@@ -11,6 +11,7 @@ static hipError_t coop_dispatch(int kind, const Args& a, hipStream_t st) {
     case CK_SLICE_FWD: hipLaunchKernelGGL(k_coop_slice_fwd<T>, grid, blk, 0, st, a); break;
     case CK_SLICE_BWD: hipLaunchKernelGGL((k_coop_bwd<T, true>), grid, blk, 0, st, a); break;
     case CK_DESLICE_BWD: hipLaunchKernelGGL((k_coop_bwd<T, false>), grid, blk, 0, st, a); break;
+    case CK_DESLICE_FWD: hipLaunchKernelGGL(k_coop_deslice_fwd<T>, grid, blk, 0, st, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

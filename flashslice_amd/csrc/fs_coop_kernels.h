@@ -51,6 +51,9 @@ constexpr int kPsRowB = 256 * 2 + 16;
 constexpr int kPsBufB = 32 * kPsRowB;
 static_assert(kCoopWaves * kTrPieceB + 2 * kPsBufB <= kCoopWaves * kCoopWReg * 4,
               "coop backward buffers exceed the staging regions");
+// the deslice forward's two weight buffers in the forward's staging regions
+static_assert(2 * kPsBufB <= kCoopWaves * (kCoopTr + 17 * 64) * 4,
+              "coop deslice buffers exceed the staging regions");
 constexpr int kCoopPts = 4 * kCoopWaves * 32;    // per-point exchange: 2 buffers x 2 rows per wave
 constexpr int kCoopVec = 2 * 32 * kCoopWaves;    // per-slot vectors: bias * cst, d s
 constexpr int kCoopTileB = kTrPieceB;            // one staged 32 x 32 bf16 tile (bytes)
@@ -198,13 +201,14 @@ __device__ __forceinline__ void tile_rows(Frag<MMA_BF16>& f, const char* region,
 }
 
 // Staging of the block's point tiles: threads 0..127 take x, 128..255 the
-// second stream (fx or d_out); three LDS buffers rotate, so the tile stored
-// for the next step never overwrites one a slower wave may still read.
-#define COOP_STAGING(FAST)                                                              \
+// second stream (fx or d_out; TWO = false: none); three LDS buffers rotate,
+// so the tile stored for the next step never overwrites one a slower wave
+// may still read.
+#define COOP_STAGING(FAST, TWO)                                                         \
   /* waves 0, 1 load x, waves 2, 3 the second stream: conditions on the   */           \
   /* (scalar) wave index, so each load sees one uniform buffer resource   */           \
   const int li_ = ((wid & 1) << 6) | lane;                                              \
-  const bool ldx_ = wid < 2, ldf_ = wid >= 2 && wid < 4;                                \
+  const bool ldx_ = wid < 2, ldf_ = (TWO) && wid >= 2 && wid < 4;                       \
   uint32_t stg_[4] = {0u, 0u, 0u, 0u};                                                  \
   /* the block's tiles in order: pid, pid + P, ... (one cursor per wave) */             \
   TileCursor gk_ = ldx_ ? tile_cursor(x_b, x_sn, x_w, pid, a.P, N)                      \
@@ -245,7 +249,7 @@ __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
   const float* st_l = st_m ? st_m + R_.NS : nullptr;
   auto run = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
-    COOP_STAGING(FAST)
+    COOP_STAGING(FAST, true)
     // per-point statistics of the block's tiles, in order (read or written)
     TileCursor km = tile_cursor(sm ? sm : st_m, 4, 4, pid, a.P, (sm || st_m) ? N : 0);
     TileCursor kl = tile_cursor(sm ? sm + R_.NS : st_l, 4, 4, pid, a.P, (sm || st_m) ? N : 0);
@@ -342,7 +346,7 @@ __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
   }
 }
 
-// ---------------------------------------------------------------- backward
+// ---------------------------------------------------------------- deslice fwd
 // A [point][slot] bf16 buffer of the block (rows of kPsRowB bytes): lane
 // (c, h) of wave wid writes its fragment f ([point c][slot 32 wid + kmap(j,
 // h)]) as four 8-byte pieces, slots 32 wid + 8 q + 4 h .. + 3.
@@ -358,6 +362,167 @@ __device__ __forceinline__ void ps_put(char* buf, const Frag<MMA_BF16>& f, int w
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// One 16-point x 16-column block of a contraction over all of a tile's slots
+// with v_mfma_f32_16x16x32_bf16 (operand lanes l supply contraction indices
+// 8 (l / 16) .. + 7, the same on both operands; output lane l holds column
+// l % 16 and rows 4 (l / 16) .. + 3): A = the wave's register operand ([16
+// columns][slots 32 ks + 8 kg + e]), B = rows of a [point][slot] buffer read
+// 16 bytes at a time. Lane (l16, kg) gets the block's point op = 16 ph + l16,
+// columns 4 kg .. + 3 (of the block's 16).
+__device__ __forceinline__ f32x4 ps_contract(const bf16x8 (&A)[kCoopWaves], const char* buf, int op,
+                                             int kg) {
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const char* brow = buf + op * kPsRowB + 16 * kg;
+#pragma unroll
+  for (int ks = 0; ks < kCoopWaves; ++ks) {
+    const bf16x8 bv = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(brow + 64 * ks));
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[ks], bv, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// A wave's register operand for ps_contract: columns 16 dh .. + 15 of a
+// (G x C) fp32 matrix src (row stride C), times sc, as [column][slot].
+__device__ __forceinline__ void ps_operand(bf16x8 (&A)[kCoopWaves], const float* src, int G, int C,
+                                           int dh, float sc, bool on, int lane) {
+  const int kg = lane >> 4, col = 16 * dh + (lane & 15);
+#pragma unroll
+  for (int ks = 0; ks < kCoopWaves; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int g = 32 * ks + 8 * kg + e;
+      A[ks][e] = (__bf16)((on && g < G && col < C) ? src[(int64_t)g * C + col] * sc : 0.f);
+    }
+}
+
+// out = w tokens: every wave forms the weights of its 32 slots and writes
+// them into the block's [point][slot] buffer (two, alternating by tile
+// parity); after the tile's barrier waves 0..3 each contract one 16 x 16
+// block of out over all slots (ps_contract) and store it, four consecutive
+// columns of one point per lane. With saved statistics w = exp2(t2 - (m2 +
+// log2 l)) and one barrier per tile; without, the waves' (max, sum) pairs
+// are combined after a first barrier (as in the slice forward) and written
+// to stats_out when asked for.
+template <typename T>
+__global__ __launch_bounds__(kCoopThreads, 2) void k_coop_deslice_fwd(Args a) {
+  COOP_PROLOGUE(kCoopWRegFwd)
+  const int ph = (wid >> 1) & 1, dh = wid & 1;
+  const bool out_ = wid < 4;
+  const int kg = lane >> 4, l16 = lane & 15;
+  bf16x8 Ao[kCoopWaves];  // tokens [v][g]
+  ps_operand(Ao, a.tok + (int64_t)bh * G * DV, G, DV, dh, 1.f, out_, lane);
+  __syncthreads();  // the staging area becomes the weight buffers
+  char* wbuf = reinterpret_cast<char*>(smem);
+  COOP_SLICE(x, a.x, a.sxb, a.sxn, a.sxh, D)
+  COOP_SLICE(f, a.x, a.sxb, a.sxn, a.sxh, D)  // no second stream (never loaded)
+  COOP_SLICE(o, a.o1, a.s1b, a.s1n, a.s1h, DV)
+  (void)x_row; (void)f_row; (void)o_row;
+  const float* sm = a.stats_in ? a.stats_in + R_.stats_off() : nullptr;
+  const float* st_m = a.stats_out ? a.stats_out + R_.stats_off() : nullptr;
+  const int op = 16 * ph + l16, oc = 16 * dh + 4 * kg;
+  auto run = [&](auto fast_c) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    COOP_STAGING(FAST, false)
+    // statistics (saved ones, read one tile ahead; or computed ones,
+    // written by wave 0) and out, the block's tiles in order
+    const float* srow = sm ? sm : st_m;
+    TileCursor km = tile_cursor(srow, 4, 4, pid, a.P, srow ? N : 0);
+    TileCursor kl = tile_cursor(srow ? srow + R_.NS : nullptr, 4, 4, pid, a.P, srow ? N : 0);
+    TileCursor ko = tile_cursor(o_b, o_sn, o_w, pid, a.P, N);
+    const uint32_t ooff = (uint32_t)(op * o_sn) + (uint32_t)(oc * (int)sizeof(T));
+    float smv[2] = {0.f, 0.f}, slv[2] = {0.f, 0.f};
+    auto sload = [&](int q) {
+      smv[q] = ld_pt(km.rsrc(), c);
+      slv[q] = ld_pt(kl.rsrc(), c);
+      km.next();
+      kl.next();
+    };
+    auto body = [&](int t, int cur, auto par) {
+      const bool pv = t * kTile + c < N;
+      constexpr float sg = decltype(par)::sign;
+      constexpr int q = sg < 0.f ? 1 : 0;
+      char* wb = wbuf + q * kPsBufB;
+      Frag<M> xq;
+      tile_rows(xq, tile_at(cur, 0), c, h);
+      float t2[16], w[16];
+      COOP_LOGITS(t2, xq)
+      if (sm) {
+        const float sh = pv ? fmaf(smv[q], kLog2e, __builtin_amdgcn_logf(slv[q])) : kFarShift;
+        sload(q ^ 1);  // t + P
+#pragma unroll
+        for (int r = 0; r < 16; ++r) w[r] = __builtin_amdgcn_exp2f(t2[r] - sh);
+        lstore(cur == 2 ? 0 : cur + 1);  // publish the next tile
+      } else {
+        float m = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m = fmaxf(m, t2[r]);
+        m = pair_max(m);
+        float ls = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          w[r] = __builtin_amdgcn_exp2f(t2[r] - m);
+          ls += w[r];
+        }
+        ls = pair_sum(ls);
+        float* xb = xpt + q * 2 * kCoopWaves * 32;
+        if (h == 0) {
+          xb[wid * 32 + c] = m;
+          xb[kCoopWaves * 32 + wid * 32 + c] = ls;
+        }
+        lstore(cur == 2 ? 0 : cur + 1);  // publish the next tile
+        __syncthreads();
+        float m2 = xb[c];
+#pragma unroll
+        for (int wv = 1; wv < kCoopWaves; ++wv) m2 = fmaxf(m2, xb[wv * 32 + c]);
+        float l = 0.f;
+#pragma unroll
+        for (int wv = 0; wv < kCoopWaves; ++wv)
+          l += xb[kCoopWaves * 32 + wv * 32 + c] * __builtin_amdgcn_exp2f(xb[wv * 32 + c] - m2);
+        if (wid == 0 && st_m) store_stats_at(km.rsrc(), kl.rsrc(), c, h, m2, l);
+        km.next();
+        kl.next();
+        const float inv = pv ? __builtin_amdgcn_exp2f(m - m2) * __builtin_amdgcn_rcpf(l) : 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) w[r] *= inv;
+      }
+      Frag<M> wq;
+      prep<M>(wq, w);
+      ps_put(wb, wq, wid, c, h);
+      __syncthreads();
+      gload();  // t + 2 P
+      const Rsrc ro = ko.rsrc();
+      ko.next();
+      if (out_) {
+        const f32x4 acc = ps_contract(Ao, wb, op, kg);
+        if (FAST) {
+          Buf<T>::st4(ro, ooff, acc[0], acc[1], acc[2], acc[3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            Buf<T>::st1(ro, oc + r < DV ? ooff + (uint32_t)(r * (int)sizeof(T)) : kOff, acc[r]);
+        }
+      }
+    };
+    int t = pid, cur = 0;
+    gload();  // t
+    lstore(0);
+    gload();  // t + P
+    if (sm) sload(0);  // t
+    __syncthreads();
+    while (t < ntiles_) {
+      body(t, cur, TileEven());
+      t += a.P;
+      cur = cur == 2 ? 0 : cur + 1;
+      if (t >= ntiles_) break;
+      body(t, cur, TileOdd());
+      t += a.P;
+      cur = cur == 2 ? 0 : cur + 1;
+    }
+  };
+  if (fast) run(std::true_type()); else run(std::false_type());
+}
+
+// ---------------------------------------------------------------- backward
 // One pass of the slice (SLICE) or deslice backward from saved statistics:
 // omega = fx . dz_num + d s (slice) or d_out . tokens (deslice); delta and
 // Lb = w (omega - delta) per point; dx = Lb W / tau and (slice) dfx =
@@ -367,13 +532,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // dx and dfx contract over all G slots, which the eight waves hold 32 each:
 // every wave writes its Lb (and w) into the block's [point][slot] buffers,
 // and after the tile's second barrier four waves per output each compute a
-// 16-point x 16-column block of it over all slots with
-// v_mfma_f32_16x16x32_bf16 (operand lanes l supply contraction indices
-// 8 (l / 16) .. + 7, the same on both operands; output lane l holds column
-// l % 16 and rows 4 (l / 16) .. + 3): A = (W / tau) [d][g] or dz_num [v][g],
-// held in registers for the whole pass, B = the buffer's [g][p] read in
-// 16-byte rows. The sum over slots is the MFMA's own, in a fixed order, and
-// each lane stores four consecutive columns of one point.
+// 16-point x 16-column block of it over all slots (ps_contract; A = (W /
+// tau) [d][g] or dz_num [v][g], held in registers for the whole pass). The
+// sum over slots is the MFMA's own, in a fixed order, and each lane stores
+// four consecutive columns of one point.
 template <typename T, bool SLICE>
 __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
   COOP_PROLOGUE(kCoopWReg)
@@ -397,18 +559,8 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
   const bool out_ = SLICE || wid < 4;
   const int kg = lane >> 4, l16 = lane & 15;
   bf16x8 Ao[kCoopWaves];
-  {
-    const float* src = os == 0 ? Wp : a.tok + (int64_t)bh * G * DV;
-    const int C = os == 0 ? D : DV, col = 16 * dh + l16;
-    const float sc = os == 0 ? inv_tau : 1.f;
-#pragma unroll
-    for (int ks = 0; ks < kCoopWaves; ++ks)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int g = 32 * ks + 8 * kg + e;
-        Ao[ks][e] = (__bf16)((out_ && g < G && col < C) ? src[(int64_t)g * C + col] * sc : 0.f);
-      }
-  }
+  ps_operand(Ao, os == 0 ? Wp : a.tok + (int64_t)bh * G * DV, G, os == 0 ? D : DV, dh,
+             os == 0 ? inv_tau : 1.f, out_, lane);
   __syncthreads();  // the staging regions become the transpose regions and buffers
   char* trB = reinterpret_cast<char*>(smem) + wid * kTrPieceB;
   char* lbuf = reinterpret_cast<char*>(smem) + kCoopWaves * kTrPieceB;
@@ -430,7 +582,7 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
   const int oC = os == 0 ? D : DV;
   auto run = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
-    COOP_STAGING(FAST)
+    COOP_STAGING(FAST, true)
     // the statistics of a wave's tiles, loaded one tile ahead (a load waited
     // for in the same tile would expose a whole memory latency per tile);
     // [parity]: the even / odd bodies of the unrolled loop
@@ -522,13 +674,7 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
       const Rsrc ro = ko.rsrc();
       ko.next();
       if (out_) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        const char* brow = obuf + op * kPsRowB + 16 * kg;
-#pragma unroll
-        for (int ks = 0; ks < kCoopWaves; ++ks) {
-          const bf16x8 bv = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(brow + 64 * ks));
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ao[ks], bv, acc, 0, 0, 0);
-        }
+        const f32x4 acc = ps_contract(Ao, obuf, op, kg);
         if (FAST) {
           Buf<T>::st4(ro, ooff, acc[0], acc[1], acc[2], acc[3]);
         } else {

@@ -167,7 +167,7 @@ int blocked_width_blocks(int D, int DV);  // 1, 2, 4 or 8 (0 if D or DV > 256)
 // of eight waves takes one point tile at a time, wave w slots 32 w ..; grid
 // (P, B * H) with a.P = the blocks per (b, h); one partial per block in the
 // whole-G layout (part_floats_*). The backward kernels need statistics.
-enum CoopKind { CK_SLICE_FWD = 0, CK_SLICE_BWD = 1, CK_DESLICE_BWD = 2 };
+enum CoopKind { CK_SLICE_FWD = 0, CK_SLICE_BWD = 1, CK_DESLICE_BWD = 2, CK_DESLICE_FWD = 3 };
 hipError_t launch_coop(int kind, const Args& a, int dtype, hipStream_t st);
 
 // Waves per SIMD the whole-G slice forward is compiled for, by its blocks of

@@ -218,7 +218,7 @@ def test_stats_modes_agree():
 
 # ------------------------------------------------ block-cooperative kernels
 # bf16 dots on bf16 point tensors at 128 < G <= 256 (D, DV <= 32) run the
-# G-blocked family's block-cooperative kernels (slice forward and both
+# G-blocked family's block-cooperative kernels (both forward and both
 # backward passes in one pass each); these cases cover partial last waves
 # (G not a multiple of 32 * 8), narrow widths, tiny N, both call orders
 # (statistics formed in the slice's pass, or handed in by the deslice) and
