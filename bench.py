@@ -2,39 +2,42 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
                     [--workload c1|c2|c2-df|c3-256|c3-1024|c4|c5|c5-262k|ragged|layer|layer-1m-fwd]
-                    [--tied]
+                    [--backward auto|tied|two-op]
 
 One step is the coupling the metric names ("slice+deslice
-fwd+bwd ms & Mpoints/s at N=1M, H=8, D=32, G=32; peak HBM"): the four
-``torch.ops.flashslice`` operators on one batch of synthetic points already
-resident in HBM, in the order autograd runs them --
+fwd+bwd ms & Mpoints/s at N=1M, H=8, D=32, G=32; peak HBM") on one batch of
+synthetic points already resident in HBM, through the ``torch.ops.flashslice``
+operators, in the order autograd runs them:
 
-    z_num, s   = flash_slice(x, fx, W, b, tau)           slice forward
+    z_num, s   = slice(x, fx, W, b, tau)                 slice forward
     tokens     = z_num / (s + 1e-5)                      (torch, tiny)
-    out        = flash_deslice(x, W, b, tau, tokens)     deslice forward
-    dx1, dtok, dW1, db1, dtau1 = flash_deslice_bwd(..., d_out)
-    dz, ds     = chain rule through tokens               (torch, tiny)
-    dx2, dfx, dW2, db2, dtau2 = flash_slice_bwd(..., dz, ds)
+    out        = deslice(x, W, b, tau, tokens)           deslice forward
+    backward of both, with upstream gradients d_out, dz_num, ds ~ N(0, 1)
+    (the loss of reference bench/parity_ops.py:148-151) and the chain rule
+    through the tokens (torch, tiny)
 
-with upstream gradients d_out, dz_num, ds ~ N(0, 1) (the loss of reference
-bench/parity_ops.py:148-151). Inputs follow BASELINE.json config 2: x, fx
-~ N(0, 1) (1, 1e6, 8, 32) fp32; per-head W ~ N(0, 1/D); b ~ N(0, 0.02^2);
-tau ~ U[0.3, 1.0]. ``value`` is points per second of the whole step.
+The backward takes one of two forms, with the same gradients:
+  * tied (the default where the whole-G kernels serve the shape, as at C2):
+    the operators ``fused_coupling`` runs -- the deslice's dtokens (the slice
+    forward kernel on d_out), then one merged pass for the rest of both
+    backwards (dx of both ops summed, dfx, dW, db, dtau);
+  * two ops (reference slice_ops.py:822-885): flash_deslice_bwd, then
+    flash_slice_bwd (whose two dx autograd would still have to add).
+Either way the step moves the same 11 x-sized passes of algorithmic bytes.
+Where both forms exist the line reports the other one too
+(``other_backward``). Inputs follow BASELINE.json config 2: x, fx ~ N(0, 1)
+(1, 1e6, 8, 32) fp32; per-head W ~ N(0, 1/D); b ~ N(0, 0.02^2); tau ~
+U[0.3, 1.0]. ``value`` is points per second of the whole step.
 
 Printed: ONE JSON line with the driver's fields, plus ``roofline`` (the
 dominant op's algorithmic bytes per launch over its HIP-event time on its
 stream -- the op is its point kernel and the small fixed-order reduction of
 its partials; ``traffic`` is the HBM bytes rocprofv3 counted for it, from
-the committed profiles/<workload>_hbm_traffic.txt), ``step_roofline`` (all
-four ops' algorithmic bytes over the step), ``cpu_baseline`` (the CPU
+the committed profiles/<workload>[-tied]_hbm_traffic.txt), ``step_roofline``
+(the step's algorithmic bytes over its time), ``cpu_baseline`` (the CPU
 oracle -- the eager PyTorch softmax/einsum path -- timed on a bounded sample
-on this host's cores), ``peak_hbm_gb``, ``per_op_ms`` and
-``deterministic``.
-
-``--tied`` times the step with the backward ``fused_coupling`` runs: the
-same gradients through the tied kernel (slice-first: the deslice's dtokens
-pass first, since the token step needs dtokens before the slice's backward;
-then one pass for everything else), its ops in ``per_op_ms``.
+on this host's cores), ``peak_hbm_gb``, ``per_op_ms``, ``deterministic`` and
+``public_api`` (the same step through the public API and autograd).
 """
 
 import argparse
@@ -107,6 +110,40 @@ LAYER_WORKLOADS = {
 }
 # dot level per run (reference slice_ops.py:336-343): 0 ieee; 3 bf16 (bf16 inputs)
 DOTS = {"ieee": 0, "bf16": 3}
+
+
+def timing_events(n):
+    """n timing events, each recorded once already: the runtime creates an
+    event on its first record, so the timed loop must not be the first to
+    record them (measured: one host stall of ~38 ms inside one op of the
+    timed steps when 200 fresh events were first recorded there)."""
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    for e in ev:
+        e.record()
+    torch.cuda.synchronize()
+    return ev
+
+
+def event_pairs(n):
+    ev = timing_events(2 * n)
+    return list(zip(ev[0::2], ev[1::2]))
+
+
+class quiet_gc:
+    """Collect, then keep Python's garbage collector out of the timed region
+    (a full collection in a torch process is tens of ms of host time, which
+    the GPU spends idle once the launch queue has drained)."""
+
+    def __enter__(self):
+        import gc
+        gc.collect()
+        self.was = gc.isenabled()
+        gc.disable()
+
+    def __exit__(self, *exc):
+        import gc
+        if self.was:
+            gc.enable()
 
 
 def make_inputs(B, N, H, D, DV, G, layout, device, seed=0):
@@ -232,10 +269,15 @@ def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", dot=0
         dx1, dtok, dW1, db1, dt1 = timed("deslice_bwd", deslice_b, tok0, st)
         return z, s, out, dx1, dtok, dW1, db1, dt1, dx2, dfx, dW2, db2, dt2
     if tied:
-        z, s, st = timed("slice_fwd", ops.slice_blk, x, fx, W, b, tau, None, dot)
+        # the operators fused_coupling runs (kernels/coupling.py): the slice
+        # first (statistics for the G-blocked kernels, a placeholder where the
+        # whole-G kernels serve the shape), the deslice after it, then the
+        # deslice's backward (dtokens: the slice forward kernel on d_out) and
+        # one merged pass for the rest of both backwards
+        z, s, st, lp, lt = timed("slice_fwd", ops.tied_slice, x, fx, W, b, tau, dot)
         den = (s + EPS)[..., None]
         tok = z / den
-        out, _ = timed("deslice_fwd", ops.deslice_blk, x, W, b, tau, tok, st, dot)
+        out = timed("deslice_fwd", ops.tied_deslice_after, x, W, b, tau, tok, st, lp, lt, dot)
         dtok, _, _ = timed("dtok_pass", ops.slice_blk, x, d_out, W, b, tau, st, dot)
         dz = dzb + dtok / den
         ds = dsb - (dtok * tok).sum(-1) / den[..., 0]
@@ -291,14 +333,13 @@ def time_public(inputs, order, steps, warmup):
         for _ in range(warmup):
             public_step(*inputs, order, cp)
         grads[name] = public_step(*inputs, order, cp)
-        ts = []
-        for _ in range(steps):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            public_step(*inputs, order, cp)
-            e1.record()
-            ts.append((e0, e1))
-        torch.cuda.synchronize()
+        ts = event_pairs(steps)
+        with quiet_gc():
+            for e0, e1 in ts:
+                e0.record()
+                public_step(*inputs, order, cp)
+                e1.record()
+            torch.cuda.synchronize()
         ms = sorted(e0.elapsed_time(e1) for e0, e1 in ts)
         res[name + "_ms"] = round(ms[len(ms) // 2], 4)
     diff = max(float((u.double() - v.double()).norm() / v.double().norm().clamp_min(1e-30))
@@ -406,12 +447,13 @@ def bench_ragged(a, cfg):
     def timed(fn, k):
         for _ in range(a.warmup):
             fn()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(k):
-            fn()
-        torch.cuda.synchronize()
-        return 1e3 * (time.perf_counter() - t0) / k
+        with quiet_gc():
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(k):
+                fn()
+            torch.cuda.synchronize()
+            return 1e3 * (time.perf_counter() - t0) / k
 
     r1 = [t.clone() for t in ragged()]
     deterministic = all(torch.equal(u, v) for u, v in zip(r1, ragged()))
@@ -462,16 +504,16 @@ def bench_c1(a):
 
     for _ in range(a.warmup):
         step()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(a.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for e0, e1 in ev:
-        e0.record()
-        res = step()
-        e1.record()
-    torch.cuda.synchronize()
-    ms = 1e3 * (time.perf_counter() - t0) / a.steps
+    ev = event_pairs(a.steps)
+    with quiet_gc():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for e0, e1 in ev:
+            e0.record()
+            res = step()
+            e1.record()
+        torch.cuda.synchronize()
+        ms = 1e3 * (time.perf_counter() - t0) / a.steps
     ms_med = sorted(e0.elapsed_time(e1) for e0, e1 in ev)[a.steps // 2]
     ref = oracle.coupling(x.double(), fx.double(), W.double(), None, tau.double(),
                           order="slice-first")
@@ -632,16 +674,16 @@ def bench_model(a, cfg):
     step()
     torch.cuda.synchronize()
     peak_gb = (torch.cuda.max_memory_allocated() - base) / 1e9
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(a.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for e0, e1 in ev:
-        e0.record()
-        step()
-        e1.record()
-    torch.cuda.synchronize()
-    ms_step = 1e3 * (time.perf_counter() - t0) / a.steps
+    ev = event_pairs(a.steps)
+    with quiet_gc():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for e0, e1 in ev:
+            e0.record()
+            step()
+            e1.record()
+        torch.cuda.synchronize()
+        ms_step = 1e3 * (time.perf_counter() - t0) / a.steps
     ms_ev = sum(e0.elapsed_time(e1) for e0, e1 in ev) / a.steps
     flops = model_flops(model, cfg, N)
     tf = flops / (ms_ev * 1e-3) / 1e12
@@ -700,10 +742,12 @@ def main():
                     + sorted(LAYER_WORKLOADS) + ["c1"])
     ap.add_argument("--dot", default="ieee", choices=sorted(DOTS),
                     help="dot level: ieee (fp32 inputs) or bf16 (x_mid, fx_mid, W in bf16)")
-    ap.add_argument("--tied", action="store_true",
-                    help="the backward as fused_coupling runs it instead of the two backward "
-                         "ops: deslice-first one tied pass; slice-first the dtokens pass, then "
-                         "one tied pass")
+    ap.add_argument("--backward", default="auto", choices=("auto", "tied", "two-op"),
+                    help="tied: the backward as fused_coupling runs it (deslice-first one tied "
+                         "pass; slice-first the dtokens pass, then one tied pass); two-op: the "
+                         "two backward ops (reference slice_ops.py:822-885); auto (default): "
+                         "tied where the whole-G kernels serve the shape, else two-op")
+    ap.add_argument("--tied", action="store_true", help="the same as --backward tied")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="before the warmup, copy x once (B*N*H*D*4 bytes read and written): "
@@ -742,10 +786,17 @@ def main():
     if a.dot == "bf16":  # reference bench/parity_ops.py:134-136: activations and W in bf16
         for i in (0, 1, 2, 3, 5):
             inputs[i] = inputs[i].bfloat16()
-    from flashslice_amd.kernels.slice_ops import _use_blocked
+    from flashslice_amd.kernels.slice_ops import _use_blocked, _whole_g
     blocked = _use_blocked(D, G, DV, dot)
-    ops_timed = ((("deslice_fwd", "slice_fwd", "tied_bwd") if order == "deslice-first" else
-                  ("slice_fwd", "deslice_fwd", "dtok_pass", "tied_bwd")) if a.tied else OPS)
+    whole = _whole_g(D, DV, G)
+    if a.tied:
+        a.backward = "tied"
+    a.tied = a.backward == "tied" or (a.backward == "auto" and whole)
+
+    def ops_of(tied):
+        return ((("deslice_fwd", "slice_fwd", "tied_bwd") if order == "deslice-first" else
+                 ("slice_fwd", "deslice_fwd", "dtok_pass", "tied_bwd")) if tied else OPS)
+    ops_timed = ops_of(a.tied)
     run_step = functools.partial(step_ops, *inputs, order=order, dot=dot, blocked=blocked,
                                  tied=a.tied)
     torch.cuda.synchronize()
@@ -761,9 +812,14 @@ def main():
               flush=True)
         del probe
 
-    for _ in range(a.warmup):
-        run_step()
-    torch.cuda.synchronize()
+    # the timed region's events, created (and recorded once) before any step:
+    # the host work of creating them then leaves no idle gap before the timed
+    # steps
+    pairs = iter(event_pairs(a.steps * (len(ops_timed) + 1)))
+    evs = [{n: next(pairs) for n in ops_timed} for _ in range(a.steps)]
+    sev = [next(pairs) for _ in range(a.steps)]
+    gc_quiet = quiet_gc()
+    gc_quiet.__enter__()
 
     # determinism: two steps bitwise equal
     r1 = [t.clone() for t in run_step()]
@@ -780,11 +836,10 @@ def main():
     peak_gb = (torch.cuda.max_memory_allocated() - base) / 1e9
     del res
 
-    # timed region: K steps, per-op HIP events on the launch stream
-    evs = [{n: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for n in ops_timed} for _ in range(a.steps)]
-    sev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(a.steps)]
+    # timed region: K steps, per-op HIP events on the launch stream, right
+    # after the W warmup steps
+    for _ in range(a.warmup):
+        run_step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(a.steps):
@@ -793,9 +848,38 @@ def main():
         sev[i][1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    # the other form of the backward where the whole-G kernels serve both
+    # (the two backward ops against the merged one), the same K steps after
+    # W warmup steps, HIP-event timed
+    alt = None
+    if whole:
+        alt_tied = not a.tied
+        alt_ops = ops_of(alt_tied)
+        run_alt = functools.partial(step_ops, *inputs, order=order, dot=dot, blocked=blocked,
+                                    tied=alt_tied)
+        apairs = iter(event_pairs(a.steps * (len(alt_ops) + 1)))
+        aevs = [{n: next(apairs) for n in alt_ops} for _ in range(a.steps)]
+        asev = [next(apairs) for _ in range(a.steps)]
+        for _ in range(a.warmup):
+            run_alt()
+        for i in range(a.steps):
+            asev[i][0].record()
+            run_alt(ev=aevs[i])
+            asev[i][1].record()
+        torch.cuda.synchronize()
+        ams = sorted(e0.elapsed_time(e1) for e0, e1 in asev)
+        alt = {"backward": "tied" if alt_tied else "two ops",
+               "ms_per_step_median": round(ams[len(ams) // 2], 4),
+               "per_op_ms": {n: round(sum(e[n][0].elapsed_time(e[n][1]) for e in aevs)
+                                      / a.steps, 4) for n in alt_ops}}
+    gc_quiet.__exit__(None, None, None)
     ms_step = 1e3 * wall / a.steps
     step_ms = sorted(e0.elapsed_time(e1) for e0, e1 in sev)
     ms_median = step_ms[len(step_ms) // 2]
+    print("[bench] event-timed steps: min %.4f median %.4f max %.4f ms; wall mean %.4f ms; "
+          "in order: %s" % (step_ms[0], ms_median, step_ms[-1], 1e3 * wall / a.steps,
+                            " ".join("%.3f" % e0.elapsed_time(e1) for e0, e1 in sev)),
+          file=sys.stderr, flush=True)
     per_op = {n: sum(e[n][0].elapsed_time(e[n][1]) for e in evs) / a.steps for n in ops_timed}
     bytes_ = alg_bytes(B, N, H, D, DV, 2 if a.dot == "bf16" else 4)
     flops = alg_flops(B, N, H, D, DV, G)
@@ -862,6 +946,7 @@ def main():
         "peak_hbm_gb": round(peak_gb, 3),
         "nxhxg_gb": round(B * N * H * G * 4 / 1e9, 3),
         "deterministic": deterministic,
+        "other_backward": alt,
         "public_api": public,
         "cpu_baseline": cpu,
     }

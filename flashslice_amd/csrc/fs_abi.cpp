@@ -910,6 +910,7 @@ int32_t fs_tied_bwd(const fs_points* x, const fs_points* fx, const fs_points* d_
   a.tok2 = tokens;
   a.ds = ds;
   a.part = ws.part;
+  a.no_dtok = dtokens == nullptr;
   rc = hip_check(fs::launch_fused_tied_bwd(a, x->dtype, mode, st), who);
   if (rc) return rc;
   fs::ReduceSegments rs{};

@@ -1122,6 +1122,174 @@ __global__ __launch_bounds__(256, (NGB * NDB * NVB == 1) ? 2 : 1) void k_fused_t
   });
 }
 
+// ------------------------------------------- tied bwd without dtokens, TR
+// The tied backward of a slice -> deslice coupling (slice-first: dtokens has
+// been formed before this pass, by the slice forward kernel on d_out, and
+// is not asked for) at one block of 32 on every axis (C2's shape): the
+// slice backward's tile body (TR form of k_fused_slice_bwd: x^T and Lb^T
+// from split pieces read back transposed, db on the matrix cores) with the
+// deslice's Jacobian input added to omega: omega = fx . dz_num + d_out .
+// tokens + ds. Per tile: 5 bf16x6 splits (x, fx, d_out, w, Lb) and 78 bf16
+// MFMAs, against k_fused_tied_bwd's general body, which also forms d_out^T
+// and w^T for dtokens (two more splits, 12 more MFMAs) and splits x and Lb
+// again for their transposes. Partials in the deslice-bwd layout, the
+// dtokens part left unwritten.
+template <typename T, int DK>
+__global__ __launch_bounds__(256, 2) void k_fused_tied_nodt(Args a) {
+  constexpr int NGB = 1, NDB = 1, NVB = 1;
+  FS_PROLOGUE(NGB, NDB, NVB, 4, tr_wave_floats<DK>())
+  char* trX = reinterpret_cast<char*>(lds);
+  char* trS = trX + tr_bytes<ML>();
+  // dz_num as [g-outer, v-inner] (omega) and [v-outer, g-inner] (dfx),
+  // tokens as [g-outer, v-inner] (omega), W / tau as [d-outer, g-inner] (dx)
+  u32x4* qZr = qV;
+  u32x4* qZc = qV + FWV;
+  u32x4* qTr = qV + 2 * FWV;
+  u32x4* qWc = qV + 3 * FWV;
+  build_frags<MV>(qZr, 1, wid, lane, [&](int, float(&f)[16]) {
+    lds_frag_rowouter(f, sV, SM::SV, 0, 0, c, h);
+  });
+  if (wid == 1) {
+    float f[16];
+    lds_frag_colouter(f, sV, SM::SV, 0, 0, c, h);
+    Frag<MV> q;
+    prep<MV>(q, f);
+    lds_put<MV>(qZc, q, lane);
+  } else if (wid == 2) {
+    float f[16];
+    lds_frag_colouter(f, sW, SM::SW, 0, 0, c, h);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) f[j] *= inv_tau;
+    Frag<MV> q;
+    prep<MV>(q, f);
+    lds_put<MV>(qWc, q, lane);
+  }
+  for (int i = threadIdx.x; i < SM::GP; i += 256) sDS[i] = i < G ? a.ds[(int64_t)bh * G + i] : 0.f;
+  // the staging area now takes the tokens (dz_num's fragments are built)
+  __syncthreads();
+  stage_matrix(sV, SM::SV, a.tok2 + (int64_t)bh * G * DV, G, DV, SM::GP, 32);
+  __syncthreads();
+  if (wid == 3) {
+    float f[16];
+    lds_frag_rowouter(f, sV, SM::SV, 0, 0, c, h);
+    Frag<MV> q;
+    prep<MV>(q, f);
+    lds_put<MV>(qTr, q, lane);
+  }
+  FS_PROLOGUE_END
+  f32x16 dW[1][1];
+  dW[0][0] = zero16();
+  float dbacc[1] = {0.f}, dtacc = 0.f;
+  FS_SLICE(x, a.x, a.sxb, a.sxn, a.sxh, D)
+  FS_SLICE(f, a.f, a.sfb, a.sfn, a.sfh, DV)
+  FS_SLICE(g, a.g, a.sgb, a.sgn, a.sgh, DV)
+  FS_SLICE(dx, a.o1, a.s1b, a.s1n, a.s1h, D)
+  FS_SLICE(df, a.o2, a.s2b, a.s2n, a.s2h, DV)
+  (void)dx_row; (void)df_row;
+  uint32_t vcx[1], vcf[1];
+  vcx[0] = col_off<T>(0, D, dx_sn, c, h);
+  vcf[0] = col_off<T>(0, DV, df_sn, c, h);
+  auto run = [&](auto fast_c) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
+    const uint32_t vrf = FAST ? f_row + 4 * h * (uint32_t)sizeof(T) : f_row;
+    const uint32_t vrg = FAST ? g_row + 4 * h * (uint32_t)sizeof(T) : g_row;
+    // x is double-buffered; fx and d_out have one buffer each, reloaded for
+    // the wave's next tile as soon as each is split
+    float xA[1][16], xB[1][16], ff[1][16], of[1][16];
+    auto load = [&](float (&xn)[1][16], int t) {
+      ld_rows<T, 1, FAST>(xn, rows_rsrc_sel(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
+    };
+    auto load_f = [&](int t) {
+      ld_rows<T, 1, FAST>(ff, rows_rsrc_sel(f_b, f_sn, f_w, (int64_t)t * kTile, N), vrf, DV, h);
+    };
+    auto load_g = [&](int t) {
+      ld_rows<T, 1, FAST>(of, rows_rsrc_sel(g_b, g_sn, g_w, (int64_t)t * kTile, N), vrg, DV, h);
+    };
+    auto body = [&](const float (&xf)[1][16], int t, auto par) {
+      const int64_t p0 = (int64_t)t * kTile;
+      const bool pv = p0 + c < N;
+      constexpr float sg = decltype(par)::sign;
+      float t2[1][16], w[1][16], m2, lsum;
+      float om[1][16];
+      // Four regions pair an MFMA chain with independent VALU work: the
+      // logits with fx's split, fx . dz_num with d_out's split, d_out .
+      // tokens with the softmax, dfx with the Jacobian (sched_mfma_valu).
+      Frag<ML> xq[1];
+      prep<ML>(xq[0], xf[0]);
+      tr_put<ML>(trX, xq[0], c, h, 0u);
+      sched_fence();
+      FS_LOGITS(t2, xq)
+      Frag<MV> fq;
+      prep<MV>(fq, ff[0]);
+      sched_mfma_valu<12, 5>();
+      sched_fence();
+      load_f(t + a.P);
+      sched_fence();
+      f32x16 o;
+      {
+        Frag<MV> zq;
+        lds_get<MV>(zq, qZr, lane);
+        o = mma<MV>(zq, fq, zero16());
+      }
+      Frag<MV> gq;
+      prep<MV>(gq, of[0]);
+      sched_mfma_valu<12, 5>();
+      sched_fence();
+      load_g(t + a.P);
+      sched_fence();
+      {
+        Frag<MV> tq;
+        lds_get<MV>(tq, qTr, lane);
+        o = mma<MV>(tq, gq, o);
+      }
+      softmax_tile<NGB>(w, m2, lsum, t2, pv);
+      sched_mfma_valu<12, 7>();
+      sched_fence();
+      {
+        float dsv[16];  // d s per output slot
+        lds_frag_vec(dsv, sDS, h);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) om[0][r] = o[r] + dsv[r];
+      }
+      // dfx = w dz_num (no dfx wanted, a.o2 null: an empty range drops the stores)
+      Frag<MV> wq;
+      prep<MV>(wq, w[0]);
+      sched_fence();
+      {
+        Frag<MV> zq;
+        lds_get<MV>(zq, qZc, lane);
+        const f32x16 df = mma<MV>(wq, zq, zero16());
+        st_cols<T>(rows_rsrc_sel(df_b, df_sn, df_w, p0, a.o2 ? N : 0), vcf[0], (uint32_t)df_sn,
+                   df);
+      }
+      dtacc += jacobian_tile<NGB>(om, w, t2, pv, h);
+      sched_mfma_valu<12, 6>();
+      sched_fence();
+      FS_DX_DW_TR(om, qWc, sg)
+    };
+    load_f(pid);
+    load_g(pid);
+    FS_TILE_LOOP(load, body, true, xA, xB)
+  };
+  if (fast) run(std::true_type()); else run(std::false_type());
+  const float dbs = dbacc[0] * inv_tau;  // row_sums gave both lane halves the whole tile's sum
+  const float dt = -kLn2 * inv_tau * half_wave_sum(dtacc);
+  const int64_t offW = (int64_t)G * DV, E = part_floats_deslice_bwd(G, D, DV);
+  float* pw = a.part + ((int64_t)bh * gridDim.x + blockIdx.x) * E;
+  block_partial(smem, (int)(E - offW), wid, pw + offW, [&](float* buf, bool first) {
+    if (c < G) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = kmap(r, h);
+        if (d < D) acc_put(buf[c * D + d], dW[0][0][r] * inv_tau, first);
+      }
+      if (h == 0) acc_put(buf[G * D + c], dbs, first);
+    }
+    if (lane == 0) acc_put(buf[G * D + G], dt, first);
+  });
+}
+
 // ------------------------------------------------------------ launch templates
 // (NGB, NDB, NVB): slot, logits-width and value-width blocks of 32 held in
 // registers; the fused family serves shapes whose slot-indexed accumulators
@@ -1150,6 +1318,12 @@ template <int K, typename T, int DK>
 hipError_t fused_launch(const Args& a, hipStream_t st) {
   const int g = blocks_of(a.G), d = blocks_of(a.D), v = blocks_of(a.DV);
   const dim3 grid(a.P / kWavesPerBlock, a.B * a.H), block(256);
+  if constexpr (K == FK_TIED_BWD) {
+    if (a.no_dtok && g == 1 && d == 1 && v == 1) {
+      hipLaunchKernelGGL((k_fused_tied_nodt<T, DK>), grid, block, 0, st, a);
+      return hipGetLastError();
+    }
+  }
 #define FS_TRY(G_, D_, V_)                                                                    \
   if (g == G_ && d == D_ && v == V_) {                                                        \
     if constexpr (K == FK_SLICE_FWD)                                                          \

@@ -36,6 +36,7 @@ struct Args {
   int64_t rows_total;                      // rows of the ragged batch's point tensors
   int B, N, H, D, DV, G;
   int P;                                   // point partitions per (b, h), a multiple of 4
+  int no_dtok;                             // tied bwd: dtokens not asked for (not formed)
   int ntiles;                              // ceil(N / 32)
   int vec_x, vec_f, vec_1, vec_2;          // 4-element alignment of rows
   int fast;                                // all rows aligned, D and DV multiples of 32

@@ -24,7 +24,7 @@ import torch
 from . import _hip
 from .slice_ops import (set_tile_table, tile_table,  # noqa: F401
                         _hip_slice_fwd, _hip_deslice_fwd, _hip_slice_bwd, _hip_deslice_bwd,
-                        _Call, _as_points, _point_dtype)
+                        _Call, _as_points, _point_dtype, stats_placeholder)
 
 _BLOCK_G = None  # None = automatic; set_block_g overrides
 
@@ -119,8 +119,17 @@ torch.library.define(
     "-> (Tensor, Tensor, Tensor, Tensor, Tensor)")
 
 
+def _is_placeholder(stats):
+    return stats is not None and all(st == 0 for st in stats.stride())
+
+
 def _slice_blk_impl(x_mid, fx_mid, weight, bias, tau, stats, dot):
-    """flashslice::slice_blk (reference ``_slice_blk_impl``, blocked.py:1346-1368)."""
+    """flashslice::slice_blk (reference ``_slice_blk_impl``, blocked.py:1346-1368).
+    Given a coupling's placeholder for statistics no whole-G pass formed
+    (``stats_placeholder``), it returns that placeholder and forms none."""
+    if _is_placeholder(stats):
+        z_num, s, _ = _hip_slice_fwd(x_mid, fx_mid, weight, bias, tau, dot, stats_in=stats)
+        return z_num, s, stats
     if stats is None and _STATS_MODE == "two-pass":
         stats = compute_stats(x_mid, weight, bias, tau, dot)
     z_num, s, st = _hip_slice_fwd(x_mid, fx_mid, weight, bias, tau, dot,
@@ -136,6 +145,9 @@ def _slice_blk_bwd_impl(x_mid, fx_mid, weight, bias, tau, stats, dz_num, ds, dot
 def _deslice_blk_impl(x_mid, weight, bias, tau, tokens, stats, dot):
     """flashslice::deslice_blk (reference blocked.py:1406-1433): with no
     statistics in hand one online pass forms out and (m, l) both."""
+    if _is_placeholder(stats):
+        out, _ = _hip_deslice_fwd(x_mid, weight, bias, tau, tokens, dot, stats_in=stats)
+        return out, stats
     if stats is None and _STATS_MODE == "two-pass":
         stats = compute_stats(x_mid, weight, bias, tau, dot)
     out, st = _hip_deslice_fwd(x_mid, weight, bias, tau, tokens, dot,
@@ -160,7 +172,8 @@ def _(x_mid, fx_mid, weight, bias, tau, stats, dot):
     G = weight.shape[-2]
     return (x_mid.new_empty((B, H, G, fx_mid.shape[3]), dtype=torch.float32),
             x_mid.new_empty((B, H, G), dtype=torch.float32),
-            x_mid.new_empty((B, H, 2, N), dtype=torch.float32))
+            stats_placeholder(B, H, N, x_mid) if _is_placeholder(stats)
+            else x_mid.new_empty((B, H, 2, N), dtype=torch.float32))
 
 
 @torch.library.register_fake("flashslice::slice_blk_bwd")
@@ -174,7 +187,8 @@ def _(x_mid, fx_mid, weight, bias, tau, stats, dz_num, ds, dot):
 def _(x_mid, weight, bias, tau, tokens, stats, dot):
     B, N, H, D = x_mid.shape
     return (x_mid.new_empty((B, N, H, tokens.shape[3])),
-            x_mid.new_empty((B, H, 2, N), dtype=torch.float32))
+            stats_placeholder(B, H, N, x_mid) if _is_placeholder(stats)
+            else x_mid.new_empty((B, H, 2, N), dtype=torch.float32))
 
 
 @torch.library.register_fake("flashslice::deslice_blk_bwd")

@@ -43,7 +43,7 @@ or DV) run the two plain backward ops inside the merged node.
 import torch
 
 from .slice_ops import (_LIB, _check_dims, _dot_mode, _hip_deslice_bwd, _hip_deslice_fwd,
-                        _hip_slice_bwd, _hip_slice_fwd, _prep_wb)
+                        _hip_slice_bwd, _hip_slice_fwd, _prep_wb, _whole_g, stats_placeholder)
 from .tied import _hip_tied_bwd
 
 _LIB.define(
@@ -76,10 +76,20 @@ def _link(shape, like, dtype):
 
 # --------------------------------------------------------------- deslice first
 
+def _first_stats(x_mid, weight, dv):
+    """Whether the first op of a coupling forms softmax statistics for the
+    second op and the backward: the G-blocked kernels need them; where the
+    whole-G kernels serve the shape they hand on ``stats_placeholder``."""
+    return not _whole_g(x_mid.shape[3], dv, weight.shape[-2])
+
+
 def _tied_deslice_impl(x_mid, weight, bias, tau, tokens, dot):
     B, N, H, _ = x_mid.shape
     G, DV = weight.shape[-2], tokens.shape[3]
-    out, st = _hip_deslice_fwd(x_mid, weight, bias, tau, tokens, dot, want_stats=True)
+    want = _first_stats(x_mid, weight, DV)
+    out, st = _hip_deslice_fwd(x_mid, weight, bias, tau, tokens, dot, want_stats=want)
+    if not want:
+        st = stats_placeholder(B, H, N, x_mid)
     return (out, st, _link((B, N, H, DV), x_mid, x_mid.dtype),
             _link((B, H, G, DV + 1), x_mid, torch.float32))
 
@@ -121,7 +131,8 @@ def _(x_mid, weight, bias, tau, tokens, dot):
     B, N, H, _ = x_mid.shape
     G, DV = weight.shape[-2], tokens.shape[3]
     return (x_mid.new_empty((B, N, H, DV)),
-            x_mid.new_empty((B, H, 2, N), dtype=torch.float32),
+            x_mid.new_empty((B, H, 2, N), dtype=torch.float32)
+            if _first_stats(x_mid, weight, DV) else stats_placeholder(B, H, N, x_mid),
             _link((B, N, H, DV), x_mid, x_mid.dtype),
             _link((B, H, G, DV + 1), x_mid, torch.float32))
 
@@ -209,7 +220,10 @@ torch.library.register_autograd("flashslice::tied_slice_after", _tied_slice_afte
 def _tied_slice_impl(x_mid, fx_mid, weight, bias, tau, dot):
     B, N, H, _ = x_mid.shape
     G, DV = weight.shape[-2], fx_mid.shape[3]
-    z_num, s, st = _hip_slice_fwd(x_mid, fx_mid, weight, bias, tau, dot, want_stats=True)
+    want = _first_stats(x_mid, weight, DV)
+    z_num, s, st = _hip_slice_fwd(x_mid, fx_mid, weight, bias, tau, dot, want_stats=want)
+    if not want:
+        st = stats_placeholder(B, H, N, x_mid)
     return (z_num, s, st, _link((B, N, H, DV), x_mid, x_mid.dtype),
             _link((B, H, G, DV), x_mid, torch.float32))
 
@@ -247,7 +261,8 @@ def _(x_mid, fx_mid, weight, bias, tau, dot):
     G, DV = weight.shape[-2], fx_mid.shape[3]
     return (x_mid.new_empty((B, H, G, DV), dtype=torch.float32),
             x_mid.new_empty((B, H, G), dtype=torch.float32),
-            x_mid.new_empty((B, H, 2, N), dtype=torch.float32),
+            x_mid.new_empty((B, H, 2, N), dtype=torch.float32)
+            if _first_stats(x_mid, weight, DV) else stats_placeholder(B, H, N, x_mid),
             _link((B, N, H, DV), x_mid, x_mid.dtype),
             _link((B, H, G, DV), x_mid, torch.float32))
 

@@ -346,6 +346,42 @@ def _small(t, shape, name, device):
     return t.detach().to(torch.float32).contiguous()
 
 
+def _stats_arg(stats_in, shape, device):
+    """Handed-in statistics as the library reads them; None for none, and
+    for the placeholder of statistics a whole-G call never formed
+    (``stats_placeholder``: every stride 0), so that a G-blocked kernel
+    given it forms its own."""
+    if stats_in is None or all(st == 0 for st in stats_in.stride()):
+        return None
+    return _small(stats_in, shape, "stats", device)
+
+
+def stats_placeholder(B, H, N, like):
+    """A (B, H, 2, N) stand-in that carries no values (zero strides, no
+    memory) for the softmax statistics a coupling hands from its first op to
+    its second and to the backward when the whole-G kernels serve the shape:
+    they form the softmax exactly in each pass and read no statistics."""
+    return torch.empty_strided((B, H, 2, N), (0, 0, 0, 0), device=like.device,
+                               dtype=torch.float32)
+
+
+_WHOLE_G = {}
+
+
+def _whole_g(D, DV, G):
+    """True where the whole-G kernels serve a call of this shape (the
+    library's ``fs_family``, which depends on D, DV, G and the kernel mode
+    only)."""
+    family = 2 if _KERNEL_MODE == "blocked" else 0
+    key = (int(D), int(DV), int(G), family)
+    r = _WHOLE_G.get(key)
+    if r is None:
+        prm = _hip.FsSliceParams(1, 1, 1, int(D), int(DV), int(G), None, 0, 0, None, 0, 0,
+                                 None, 0, family, None, 0)
+        r = _WHOLE_G[key] = _hip.lib().fs_family(prm) == 1
+    return r
+
+
 def _check_points(x_mid, t, width, name):
     """A second point tensor of a call: x_mid's (B, N, H), ``width`` and
     device."""
@@ -370,7 +406,7 @@ def _hip_slice_fwd(x_mid, fx_mid, weight, bias, tau, dot, stats_in=None, want_st
         x, fx = _as_points(x_mid, dt), _as_points(fx_mid, dt)
         z_num = torch.empty(B, H, call.G, DV, device=x.device, dtype=torch.float32)
         s = torch.empty(B, H, call.G, device=x.device, dtype=torch.float32)
-        st_in = None if stats_in is None else _small(stats_in, sshape, "stats", x.device)
+        st_in = _stats_arg(stats_in, sshape, x.device)
         st_out = (torch.empty(sshape, device=x.device, dtype=torch.float32)
                   if want_stats and st_in is None else None)
         ws, nws = call.workspace(_hip.OP_SLICE_FWD)
@@ -390,7 +426,7 @@ def _hip_deslice_fwd(x_mid, weight, bias, tau, tokens, dot, stats_in=None, want_
         x = _as_points(x_mid, dt)
         tok = _small(tokens, (call.B, H, call.G, DV), "tokens", x.device)
         out = torch.empty(B, N, H, DV, device=x.device, dtype=dt)
-        st_in = None if stats_in is None else _small(stats_in, (B, H, 2, N), "stats", x.device)
+        st_in = _stats_arg(stats_in, (B, H, 2, N), x.device)
         st_out = (torch.empty(B, H, 2, N, device=x.device, dtype=torch.float32)
                   if want_stats and st_in is None else None)
         ws, nws = call.workspace(_hip.OP_DESLICE_FWD)
@@ -435,7 +471,7 @@ def _hip_slice_bwd(x_mid, fx_mid, weight, bias, tau, dz_num, ds, dot, stats_in=N
             torch.empty(fx_mid.shape, device=x.device, dtype=dt)
         dz = _small(dz_num, (call.B, H, call.G, DV), "dz_num", x.device)
         dsv = _small(ds, (call.B, H, call.G), "ds", x.device)
-        st_in = None if stats_in is None else _small(stats_in, (B, H, 2, N), "stats", x.device)
+        st_in = _stats_arg(stats_in, (B, H, 2, N), x.device)
         dW, db, dtau = _param_grad_buffers(call)
         ws, nws = call.workspace(_hip.OP_SLICE_BWD)
         _hip.check(_hip.lib().fs_slice_bwd(
@@ -462,8 +498,7 @@ def _hip_deslice_bwd(x_mid, weight, bias, tau, tokens, d_out, dot, stats_in=None
         dxm = torch.empty_like(x_mid, dtype=dt) if x_mid.stride(3) == 1 else \
             torch.empty(x_mid.shape, device=x.device, dtype=dt)
         tok = _small(tokens, (B, H, call.G, DV), "tokens", x.device)
-        st_in = (None if stats_in is None
-                 else _small(stats_in, (x_mid.shape[0], H, 2, N), "stats", x.device))
+        st_in = _stats_arg(stats_in, (x_mid.shape[0], H, 2, N), x.device)
         dtok = torch.empty(B, H, call.G, DV, device=x.device, dtype=torch.float32)
         dW, db, dtau = _param_grad_buffers(call)
         ws, nws = call.workspace(_hip.OP_DESLICE_BWD)

@@ -46,6 +46,11 @@ CASES = [
      "deslice-first"),
     ("g8-padded", dict(B=1, N=2049, H=4, D=32, G=8, mode="hgd"), "slice-first"),
     ("g1", dict(B=1, N=1025, H=2, D=32, G=1, mode="hgd"), "slice-first"),
+    # the deslice backward's head pairs (B * H even): a pair spanning two
+    # samples (B = 2, H = 3), and B * H odd (one head per block)
+    ("head-pair-across-samples", dict(B=2, N=2049, H=3, D=32, G=32, mode="bhgd"),
+     "slice-first"),
+    ("odd-heads", dict(B=1, N=3001, H=3, D=32, G=32, mode="hgd"), "deslice-first"),
 ]
 
 
