@@ -217,6 +217,14 @@ def measured_traffic(workload):
 OPS = ("slice_fwd", "deslice_fwd", "deslice_bwd", "slice_bwd")
 
 
+def token_grads(dzb, dsb, dtok, tok, den):
+    """The chain rule through tokens = z_num / den (den = s + eps, (..., 1)):
+    dz_num = dzb + dtok / den, ds = dsb - sum_v dtok tok / den."""
+    dz = torch.addcdiv(dzb, dtok, den)
+    ds = torch.addcdiv(dsb, (dtok * tok).sum(-1), den[..., 0], value=-1.0)
+    return dz, ds
+
+
 def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", dot=0,
              blocked=False, ev=None, tied=False):
     """One coupling step, forward and backward, through the operators the
@@ -279,8 +287,7 @@ def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", dot=0
         tok = z / den
         out = timed("deslice_fwd", ops.tied_deslice_after, x, W, b, tau, tok, st, lp, lt, dot)
         dtok, _, _ = timed("dtok_pass", ops.slice_blk, x, d_out, W, b, tau, st, dot)
-        dz = dzb + dtok / den
-        ds = dsb - (dtok * tok).sum(-1) / den[..., 0]
+        dz, ds = token_grads(dzb, dsb, dtok, tok, den)
         dx, dfx, dW, db, dt = timed("tied_bwd", ops.tied_slice_bwd, x, fx, W, b, tau, st, dz,
                                     ds, d_out, tok, dot)
         return z, s, out, dx, dtok, dW, db, dt, dfx
@@ -289,8 +296,7 @@ def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", dot=0
     tok = z / den
     out, _ = timed("deslice_fwd", deslice_f, tok, st)
     dx1, dtok, dW1, db1, dt1 = timed("deslice_bwd", deslice_b, tok, st)
-    dz = dzb + dtok / den
-    ds = dsb - (dtok * tok).sum(-1) / den[..., 0]
+    dz, ds = token_grads(dzb, dsb, dtok, tok, den)
     dx2, dfx, dW2, db2, dt2 = timed("slice_bwd", slice_b, st, dz, ds)
     return z, s, out, dx1, dtok, dW1, db1, dt1, dx2, dfx, dW2, db2, dt2
 

@@ -140,10 +140,11 @@ int64_t fused_target(int32_t op, const fs_slice_params* p) {
     case FS_OP_DESLICE_BWD: t = 512; break;
     // wider shapes: one wave per SIMD, one 125 KB block per CU at C4, one
     // dispatch round (measured at C4 against 512 / 1024 / 2048 blocks: 1 / 3 /
-    // 9 % faster); one block of 32 on every axis: two waves per SIMD, 1024
-    // blocks (C2's shape: 1.193 / 1.137 / 1.146 / 1.151 ms at 512 / 1024 /
-    // 1536 / 2048)
-    case FS_OP_TIED_BWD: t = one ? 1024 : 256; break;
+    // 9 % faster); one block of 32 on every axis: two waves per SIMD, 1536
+    // blocks (C2's shape, the transposed-piece kernel without dtokens:
+    // 1.180 / 1.119 / 1.070 / 1.057 / 1.084 ms at 512 / 768 / 1024 / 1536 /
+    // 2048)
+    case FS_OP_TIED_BWD: t = one ? 1536 : 256; break;
     // wider shapes: one dispatch round of the kernel's waves per SIMD (one
     // wave, 256 blocks; C4 at one wave: 0.973 ms against 0.995 at 512)
     case FS_OP_SLICE_FWD: {

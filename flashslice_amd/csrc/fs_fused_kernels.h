@@ -94,12 +94,15 @@ __device__ __forceinline__ void block_partial(float* buf, int E, int wid, float*
 __device__ __forceinline__ void acc_put(float& t, float v, bool first) { t = first ? v : t + v; }
 
 
-// Block prologue shared by the four kernels: head constants, LDS carve-up,
-// the fp32 staging of W and tokens / dz_num, and the logits operand W
-// [g-outer, d-inner] as ready fragments qL[gb * NDB + db] (bias * log2(e) /
-// tau per output slot in LDS, -1e30 on padded slots). The kernel
-// builds its value-mode fragments next and then calls FS_PROLOGUE_END.
-#define FS_PROLOGUE(NGB, NDB, NVB, NQV, WF)                                         \
+// Block prologue shared by the whole-G kernels: head constants and the LDS
+// carve-up (FS_PROLOGUE_DECL), then the fp32 staging of W and tokens /
+// dz_num and the logits operand W [g-outer, d-inner] as ready fragments
+// qL[gb * NDB + db] (bias * log2(e) / tau per output slot in LDS, -1e30 on
+// padded slots; FS_PROLOGUE_STAGE). The kernel builds its value-mode
+// fragments next and then calls FS_PROLOGUE_END. A kernel may issue its
+// first point loads between the two halves, so that they are in flight
+// while the block stages W (the slice forward: 1 % at C2).
+#define FS_PROLOGUE_DECL(NGB, NDB, NVB, NQV, WF)                                    \
   constexpr int ML = FModes<DK>::L, MV = FModes<DK>::V;                             \
   using SM = FLds<NGB, NDB, NVB, ML, MV, NGB * NDB, NQV, (WF)>;                    \
   __shared__ __attribute__((aligned(16))) float smem[SM::TOTAL];                    \
@@ -129,7 +132,9 @@ __device__ __forceinline__ void acc_put(float& t, float v, bool first) { t = fir
   const float cst = (float)(1.4426950408889634 / (double)tauf);                    \
   const float inv_tau = 1.f / tauf;                                                 \
   const bool fast = a.fast != 0;                                                    \
-  (void)inv_tau; (void)sV; (void)qV; (void)FWV; (void)DV; (void)sDS;               \
+  (void)inv_tau; (void)sV; (void)qV; (void)FWV; (void)DV; (void)sDS;
+
+#define FS_PROLOGUE_STAGE(NGB, NDB, NVB)                                            \
   stage_matrix(sW, SM::SW, Wp, G, D, SM::GP, 32 * NDB);                             \
   for (int i = threadIdx.x; i < SM::GP; i += 256) sBC[i] = i < G ? Bp[i] * cst : kNoSlot; \
   if (a.tok) stage_matrix(sV, SM::SV, a.tok + (int64_t)bh * G * DV, G, DV, SM::GP, 32 * NVB); \
@@ -137,6 +142,9 @@ __device__ __forceinline__ void acc_put(float& t, float v, bool first) { t = fir
   build_frags<ML>(qL, NGB * NDB, wid, lane, [&](int i, float(&f)[16]) {             \
     lds_frag_rowouter(f, sW, SM::SW, 32 * (i / NDB), 32 * (i % NDB), c, h);         \
   });
+
+#define FS_PROLOGUE(NGB, NDB, NVB, NQV, WF) \
+  FS_PROLOGUE_DECL(NGB, NDB, NVB, NQV, WF) FS_PROLOGUE_STAGE(NGB, NDB, NVB)
 
 // The staged fp32 matrices are dead once every ready fragment is built: the
 // transpose tiles reuse their space.
@@ -180,8 +188,7 @@ constexpr int fused_waves(int ngb, int ndb, int nvb) { return ngb * ndb * nvb ==
 // ------------------------------------------------------------------ slice fwd
 template <typename T, int DK, int NGB, int NDB, int NVB>
 __global__ __launch_bounds__(256, slice_fwd_waves(NGB, NDB, NVB)) void k_fused_slice_fwd(Args a) {
-  FS_PROLOGUE(NGB, NDB, NVB, 0, kLdsTile)
-  FS_PROLOGUE_END
+  FS_PROLOGUE_DECL(NGB, NDB, NVB, 0, kLdsTile)
   f32x16 zacc[NGB][NVB];
   float sacc[NGB];
 #pragma unroll
@@ -209,6 +216,11 @@ __global__ __launch_bounds__(256, slice_fwd_waves(NGB, NDB, NVB)) void k_fused_s
 #pragma unroll
       for (int vb = 0; vb < NVB; ++vb) ld_cols<T>(fn[vb], rf, vcf[vb], (uint32_t)f_sn);
     };
+    // the wave's first two tiles are in flight while the block stages W
+    load(xA, fA, pid);
+    load(xB, fB, pid + a.P);
+    FS_PROLOGUE_STAGE(NGB, NDB, NVB)
+    FS_PROLOGUE_END
     auto body = [&](const float (&xf)[NDB][16], const float (&fT)[NVB][16], int t, auto par) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
@@ -252,7 +264,7 @@ __global__ __launch_bounds__(256, slice_fwd_waves(NGB, NDB, NVB)) void k_fused_s
         sacc[gb] += s;
       }
     };
-    FS_TILE_LOOP(load, body, true, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
+    FS_TILE_LOOP_LOADED(load, body, true, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
   };
   // The wider shapes: one buffer per point stream, each reloaded for the
   // wave's next tile right after its last use (x after the logits, fx once
@@ -329,6 +341,8 @@ __global__ __launch_bounds__(256, slice_fwd_waves(NGB, NDB, NVB)) void k_fused_s
     }
   };
   if constexpr (NGB * NDB * NVB > 1) {
+    FS_PROLOGUE_STAGE(NGB, NDB, NVB)
+    FS_PROLOGUE_END
     if (fast) run_wide(std::true_type()); else run_wide(std::false_type());
   } else {
     if (fast) run(std::true_type()); else run(std::false_type());

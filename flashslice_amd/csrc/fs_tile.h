@@ -250,23 +250,34 @@ __device__ __forceinline__ void balance_prio(int t, int pid, int ntiles, int P) 
 // scope defines ntiles_, the tiles of its (b, h).
 #define FS_TILE_LOOP(LOAD, BODY, BAL, A_ARGS, B_ARGS)                                     \
   {                                                                                       \
+    LOAD(A_ARGS, pid);                                                                    \
+    LOAD(B_ARGS, pid + a.P);                                                              \
+    FS_TILE_LOOP_BODY_(LOAD, BODY, BAL, (A_ARGS), (B_ARGS))                               \
+  }
+// The same loop entered with the first two loads (tiles pid and pid + a.P
+// into A and B) already issued.
+#define FS_TILE_LOOP_LOADED(LOAD, BODY, BAL, A_ARGS, B_ARGS)                              \
+  FS_TILE_LOOP_BODY_(LOAD, BODY, BAL, (A_ARGS), (B_ARGS))
+// (A and B come parenthesised: a register set may be a comma-separated
+// list, FS_ARGS2)
+#define FS_UNPAREN_(...) __VA_ARGS__
+#define FS_TILE_LOOP_BODY_(LOAD, BODY, BAL, A_P, B_P)                                     \
+  {                                                                                       \
     int t_ = pid;                                                                         \
-    LOAD(A_ARGS, t_);                                                                     \
-    LOAD(B_ARGS, t_ + a.P);                                                               \
-    if (t_ < ntiles_) {                                                                  \
-      BODY(A_ARGS, t_, TileEven());                                                       \
-      LOAD(A_ARGS, t_ + 2 * a.P);                                                         \
-      if constexpr (BAL) balance_prio(t_, pid, ntiles_, a.P);                            \
+    if (t_ < ntiles_) {                                                                   \
+      BODY(FS_UNPAREN_ A_P, t_, TileEven());                                              \
+      LOAD(FS_UNPAREN_ A_P, t_ + 2 * a.P);                                                \
+      if constexpr (BAL) balance_prio(t_, pid, ntiles_, a.P);                             \
       t_ += a.P;                                                                          \
-      while (t_ < ntiles_) {                                                             \
-        BODY(B_ARGS, t_, TileOdd());                                                      \
-        LOAD(B_ARGS, t_ + 2 * a.P);                                                       \
-        if constexpr (BAL) balance_prio(t_, pid, ntiles_, a.P);                          \
+      while (t_ < ntiles_) {                                                              \
+        BODY(FS_UNPAREN_ B_P, t_, TileOdd());                                             \
+        LOAD(FS_UNPAREN_ B_P, t_ + 2 * a.P);                                              \
+        if constexpr (BAL) balance_prio(t_, pid, ntiles_, a.P);                           \
         t_ += a.P;                                                                        \
-        if (t_ >= ntiles_) break;                                                        \
-        BODY(A_ARGS, t_, TileEven());                                                     \
-        LOAD(A_ARGS, t_ + 2 * a.P);                                                       \
-        if constexpr (BAL) balance_prio(t_, pid, ntiles_, a.P);                          \
+        if (t_ >= ntiles_) break;                                                         \
+        BODY(FS_UNPAREN_ A_P, t_, TileEven());                                            \
+        LOAD(FS_UNPAREN_ A_P, t_ + 2 * a.P);                                              \
+        if constexpr (BAL) balance_prio(t_, pid, ntiles_, a.P);                           \
         t_ += a.P;                                                                        \
       }                                                                                   \
     }                                                                                     \
