@@ -26,8 +26,11 @@ pass of the forward kernels -- and hands its remaining inputs to the first
 op's backward, which forms both ops' dx_mid, dW, db and dtau in one pass
 (``fs_tied_bwd``: one logits recompute, one softmax Jacobian over the summed
 Jacobian inputs, one dx_mid / dW product). Point passes of a backward at
-DV = D: 2 + 4 = 6 against the two ops' 3 + 4 plus autograd's 3 for summing
-their dx_mid.
+DV = D: deslice-first 2 + 4 = 6, slice-first 2 + 5 = 7 (the merged pass
+also writes the slice's dfx), against the two ops' 3 + 4 plus autograd's 3
+for summing their dx_mid. Where the whole-G kernels serve the shape the
+first op forms no softmax statistics (they read none) and hands on a
+zero-stride placeholder instead.
 
 The hand-over rides on autograd itself: the first op also outputs two
 "link" tensors (zero-stride, no memory) that the second op takes as inputs.
