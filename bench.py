@@ -246,6 +246,7 @@ def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", dot=0
     (flashslice::tied_slice_bwd) for everything else. The forward ops carry
     the slice's statistics to the deslice and the backward."""
     ops = torch.ops.flashslice
+    from flashslice_amd.kernels.slice_ops import _whole_g, stats_placeholder
 
     def timed(name, fn, *args):
         if ev is None:
@@ -267,7 +268,12 @@ def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", dot=0
         deslice_b = lambda tk, st: ops.flash_deslice_bwd(x, W, b, tau, tk, d_out, dot)  # noqa
 
     if order == "deslice-first":
-        out, st = timed("deslice_fwd", deslice_f, tok0, None)
+        # the tied form as fused_deslice_slice runs it: where the whole-G
+        # kernels serve the shape they read no statistics, so none are formed
+        st0 = None
+        if tied and blocked and _whole_g(x.shape[3], fx.shape[3], W.shape[-2]):
+            st0 = stats_placeholder(x.shape[0], x.shape[2], x.shape[1], x)
+        out, st = timed("deslice_fwd", deslice_f, tok0, st0)
         z, s, _ = timed("slice_fwd", slice_f, st)
         if tied:
             dx, dfx, dW, db, dt, dtok = timed("tied_bwd", ops.deslice_slice_bwd, x, fx, W, b,

@@ -29,7 +29,7 @@ import torch.nn as nn
 
 from ..kernels.coupling import fused_coupling
 from ..kernels.slice_ops import fused_deslice, fused_slice, unsupported_dims
-from .basic import PointLinear
+from .basic import PointLinear, point_linear_pair
 
 logger = logging.getLogger(__name__)
 
@@ -102,8 +102,11 @@ class Physics_Attention_Irregular_Mesh(nn.Module):  # noqa: N801 (reference name
     def _forward_fused(self, x):
         B, N, _ = x.shape
         H, D = self.heads, self.dim_head
-        x_mid = self.in_project_x(x).view(B, N, H, D)
-        fx_mid = self.in_project_fx(x).view(B, N, H, D)
+        # both projections as one GEMM: x_mid and fx_mid are the column
+        # halves of its (B, N, 2 H D) result, read through their strides
+        xm, fm = point_linear_pair(x, self.in_project_x, self.in_project_fx)
+        x_mid = xm.view(B, N, H, D)
+        fx_mid = fm.view(B, N, H, D)
         tau = self.temperature.view(H)
         W, b = self.in_project_slice.weight, self.in_project_slice.bias
         if self.untied_deslice:

@@ -27,9 +27,10 @@ pytestmark = pytest.mark.gpu
 class Chain(Case):
     """A coupling whose second op's input depends on the first op's output."""
 
-    def __init__(self, *a, order="deslice-first", **k):
+    def __init__(self, *a, order="deslice-first", unaligned=False, **k):
         super().__init__(*a, **k)
         self.order = order
+        self.unaligned = unaligned
         g = torch.Generator().manual_seed(99)
         self.leaves["lin"] = torch.randn(self.DV, self.DV, generator=g) / self.DV ** 0.5
 
@@ -38,6 +39,11 @@ class Chain(Case):
         L = {k: v.detach().to(device=device, dtype=dtype).requires_grad_(True)
              for k, v in self.leaves.items()}
         x, fx, w, b, tau, tok = self.build(L, amp)
+        if self.unaligned:
+            # views one element into a wider buffer: rows that are not 16-byte
+            # aligned (the kernels' element-wise load path)
+            x = torch.cat([x[..., :1], x], -1)[..., 1:]
+            fx = torch.cat([fx[..., :1], fx], -1)[..., 1:]
         lin = L["lin"]
         if path == "oracle":
             f32 = (lambda t: None if t is None else (t.float() if amp else t))  # noqa: E731
@@ -100,6 +106,8 @@ CASES = [
     ("c4-shape-bhgd-dv64-g64", dict(B=2, N=3001, H=8, D=32, DV=64, G=64, mode="bhgd")),
     ("masked-g40-d40-dv24", dict(B=1, N=1537, H=4, D=40, DV=24, G=40, mode="hgd")),
     ("tiny-N17", dict(B=2, N=17, H=4, D=32, G=32, mode="hgd")),
+    # one block of 32 on every axis with padded slots and masked columns
+    ("padded-g8-d16-dv24", dict(B=1, N=1025, H=2, D=16, DV=24, G=8, mode="hgd")),
     # G-blocked shapes: the merged node runs the two plain backward ops
     ("g256-blocked", dict(B=1, N=2049, H=4, D=32, G=256, mode="hgd")),
 ]
@@ -125,6 +133,22 @@ def test_coupling_bf16(order):
     bf16 inputs."""
     _check(Chain(B=1, N=4097, H=8, D=32, G=32, mode="hgd", order=order), dot="bf16",
            amp=torch.bfloat16)
+
+
+@pytest.mark.parametrize("order", ["deslice-first", "slice-first"])
+def test_coupling_unaligned_rows(order):
+    """x_mid and fx_mid rows that are not 16-byte aligned: the merged
+    kernels' element-wise load path."""
+    _check(Chain(B=1, N=2049, H=4, D=32, G=32, mode="hgd", order=order, unaligned=True))
+
+
+@pytest.mark.parametrize("inputs,dot", [(torch.float16, ""), (torch.bfloat16, "bf16v")],
+                         ids=["fp16-ieee-dots", "bf16-bf16v-dots"])
+@pytest.mark.parametrize("order", ["deslice-first", "slice-first"])
+def test_coupling_half_inputs(order, inputs, dot):
+    """16-bit point tensors with fp32-accurate dots, and bf16 with bf16 value
+    dots (fp32-accurate logits): within 2x of eager on the same inputs."""
+    _check(Chain(B=1, N=4097, H=8, D=32, G=32, mode="hgd", order=order), dot=dot, amp=inputs)
 
 
 @pytest.mark.parametrize("name,kw,order", [

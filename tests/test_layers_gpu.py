@@ -28,7 +28,7 @@ import torch
 from parity import relerr
 from flashslice_amd.layers import Physics_Attention_Irregular_Mesh
 from flashslice_amd.models import Transolver
-from flashslice_amd.layers.basic import PointLinear
+from flashslice_amd.layers.basic import PointLinear, point_linear_pair
 from flashslice_amd.layers.norm import PointLayerNorm
 
 pytestmark = pytest.mark.gpu
@@ -108,6 +108,41 @@ def test_point_linear_split_k():
     rt = _run(truth, [x.double()], loss)
     for n, a, b, t in zip(["out", "weight", "bias", "x"], r1, re_, rt):
         _gate(n, a, b, t)
+
+
+def test_point_linear_pair():
+    """Two projections of one point stream as one GEMM (point_linear_pair:
+    the layer's in_project_x / in_project_fx) against the two nn.Linears and
+    float64 (the same gate): both outputs, every weight and bias gradient and
+    the summed input gradient; bitwise equal over two runs."""
+    torch.manual_seed(9)
+    M = 200_003
+    print("[point-linear-pair] M=%d" % M, flush=True)
+    l1, l2 = PointLinear(256, 256).to(DEV), PointLinear(256, 256).to(DEV)
+    r1m, r2m = torch.nn.Linear(256, 256).to(DEV), torch.nn.Linear(256, 256).to(DEV)
+    r1m.load_state_dict(l1.state_dict())
+    r2m.load_state_dict(l2.state_dict())
+    g = torch.Generator().manual_seed(10)
+    x = torch.randn(1, M, 256, generator=g).to(DEV)
+    u1 = torch.randn(1, M, 256, generator=g).to(DEV)
+    u2 = torch.randn(1, M, 256, generator=g).to(DEV)
+
+    def run(a, b, xx, pair):
+        xx = xx.detach().requires_grad_(True)
+        params = [a.weight, a.bias, b.weight, b.bias]
+        for p_ in params:
+            p_.grad = None
+        o1, o2 = point_linear_pair(xx, a, b) if pair else (a(xx), b(xx))
+        ((o1 * u1.to(o1.dtype)).sum() + (o2 * u2.to(o2.dtype)).sum()).backward()
+        return [o1.detach(), o2.detach(), xx.grad] + [p_.grad for p_ in params]
+
+    f1 = run(l1, l2, x, True)
+    f2 = run(l1, l2, x, True)
+    assert all(torch.equal(a, b) for a, b in zip(f1, f2))
+    e = run(r1m, r2m, x, False)
+    t = run(copy.deepcopy(r1m).double(), copy.deepcopy(r2m).double(), x.double(), False)
+    for n, a, b, tt in zip(["out1", "out2", "x", "w1", "b1", "w2", "b2"], f1, e, t):
+        _gate(n, a, b, tt)
 
 
 @pytest.mark.parametrize("C", [256, 512])
