@@ -166,6 +166,22 @@ int64_t fused_target(int32_t op, const fs_slice_params* p) {
   return t;
 }
 
+// Sweep direction of the whole-G kernels (Args::rev, tile_p0): the slice
+// forward and the deslice backward visit the (b, h) pairs and their tiles in
+// order, the deslice forward, the slice backward and the merged backward
+// last-first. In both orders a training step runs them in -- slice forward,
+// deslice forward, dtokens pass (the slice forward's kernel), merged
+// backward; or slice forward, deslice forward, deslice backward, slice
+// backward -- each kernel then starts on the points its predecessor touched
+// last, part of which the 256 MB last-level cache still holds. Measured on
+// C2's coupling step (three runs, two boxes): 2.298 / 2.338 / 2.326 ms
+// against 2.301 / 2.342 / 2.373 with every pass in order; the slice forward
+// and the dtokens pass gain 2-3 %, the reversed deslice forward loses ~2 %
+// (reversing the tiles alone, not the pairs, changed nothing).
+int sweep_rev(int32_t op) {
+  return op == FS_OP_DESLICE_FWD || op == FS_OP_SLICE_BWD || op == FS_OP_TIED_BWD;
+}
+
 // ------------------------------------------------------------------ checks
 int32_t check_params(const fs_slice_params* p, const char* who) {
   if (!p) return fail(FS_ERR_INVALID, "%s: params is NULL", who);
@@ -489,6 +505,7 @@ int32_t slice_fwd(const fs_points* x, const fs_points* fx, const fs_slice_params
     // handed-in statistics (of these very logits) are not needed
     g = geo_n(p, fused_target(FS_OP_SLICE_FWD, p));
     fs::Args a = base_args(p, g);
+    a.rev = sweep_rev(FS_OP_SLICE_FWD);
     set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
     set_in(p, fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
     a.vec_x = vec_ok(x);
@@ -619,6 +636,7 @@ int32_t fs_deslice_fwd(const fs_points* x, const fs_slice_params* p, const float
   if (family_of(p) == 1) {
     const Geo g = geo_n(p, fused_target(FS_OP_DESLICE_FWD, p));
     fs::Args a = base_args(p, g);
+    a.rev = sweep_rev(FS_OP_DESLICE_FWD);
     set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
     set_out(p, out, &a.o1, &a.s1b, &a.s1n, &a.s1h);
     a.vec_x = vec_ok(x);
@@ -688,6 +706,7 @@ int32_t fs_slice_bwd(const fs_points* x, const fs_points* fx, const fs_slice_par
   if (family_of(p) == 1) {
     const Geo g = geo_n(p, fused_target(FS_OP_SLICE_BWD, p));
     fs::Args a = base_args(p, g);
+    a.rev = sweep_rev(FS_OP_SLICE_BWD);
     set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
     set_in(p, fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
     set_out(p, dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
@@ -790,6 +809,7 @@ int32_t fs_deslice_bwd(const fs_points* x, const fs_slice_params* p, const float
   if (family_of(p) == 1) {
     const Geo g = geo_n(p, fused_target(FS_OP_DESLICE_BWD, p));
     fs::Args a = base_args(p, g);
+    a.rev = sweep_rev(FS_OP_DESLICE_BWD);
     set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
     set_in(p, d_out, &a.f, &a.sfb, &a.sfn, &a.sfh);
     set_out(p, dx, &a.o1, &a.s1b, &a.s1n, &a.s1h);
@@ -897,6 +917,7 @@ int32_t fs_tied_bwd(const fs_points* x, const fs_points* fx, const fs_points* d_
   const int Bb = Bo_of(p->b_stride_b, p->B), Hb = Ho_of(p->b_stride_h, p->H);
   const Geo g = geo_n(p, fused_target(FS_OP_TIED_BWD, p));
   fs::Args a = base_args(p, g);
+  a.rev = sweep_rev(FS_OP_TIED_BWD);
   set_in(p, x, &a.x, &a.sxb, &a.sxn, &a.sxh);
   set_in(p, fx, &a.f, &a.sfb, &a.sfn, &a.sfh);
   set_in(p, d_out, &a.g, &a.sgb, &a.sgn, &a.sgh);

@@ -109,7 +109,8 @@ __device__ __forceinline__ void acc_put(float& t, float v, bool first) { t = fir
   const int lane = threadIdx.x & 63;                                                \
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);                 \
   const int c = lane & 31, h = lane >> 5;                                           \
-  const int bh = blockIdx.y;                                                        \
+  /* rev: (b, h) pairs last-first too (tile_p0) */                                  \
+  const int bh = a.rev ? (int)gridDim.y - 1 - (int)blockIdx.y : (int)blockIdx.y;   \
   const int b = bh / a.H, hd = bh - b * a.H;                                       \
   const int pid = blockIdx.x * kWavesPerBlock + wid;                                \
   /* this sample's rows (row splits of a ragged batch) and per-point buffers */   \
@@ -118,6 +119,7 @@ __device__ __forceinline__ void acc_put(float& t, float v, bool first) { t = fir
   const int G = a.G, D = a.D, DV = a.DV;                                            \
   const int N = R_.N;                                                               \
   const int ntiles_ = R_.ntiles;                                                    \
+  const int rev_ = a.rev;                                                           \
   float* sW = smem;                                                                 \
   float* sV = smem + SM::GP * SM::SW;                                               \
   float* lds = smem + wid * (WF);                                                   \
@@ -210,7 +212,7 @@ __global__ __launch_bounds__(256, slice_fwd_waves(NGB, NDB, NVB)) void k_fused_s
     const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
     float xA[NDB][16], xB[NDB][16], fA[NVB][16], fB[NVB][16];
     auto load = [&](float (&xn)[NDB][16], float (&fn)[NVB][16], int t) {
-      const int64_t p0 = (int64_t)t * kTile;
+      const int64_t p0 = tile_p0(t, ntiles_, rev_);
       ld_rows<T, NDB, FAST>(xn, rows_rsrc(x_b, x_sn, x_w, p0, N), vrx, D, h);
       const Rsrc rf = rows_rsrc(f_b, f_sn, f_w, p0, N);
 #pragma unroll
@@ -222,7 +224,7 @@ __global__ __launch_bounds__(256, slice_fwd_waves(NGB, NDB, NVB)) void k_fused_s
     FS_PROLOGUE_STAGE(NGB, NDB, NVB)
     FS_PROLOGUE_END
     auto body = [&](const float (&xf)[NDB][16], const float (&fT)[NVB][16], int t, auto par) {
-      const int64_t p0 = (int64_t)t * kTile;
+      const int64_t p0 = tile_p0(t, ntiles_, rev_);
       const bool pv = p0 + c < N;
       constexpr float sg = decltype(par)::sign;
       float t2[NGB][16], w[NGB][16], m2, lsum;
@@ -276,10 +278,10 @@ __global__ __launch_bounds__(256, slice_fwd_waves(NGB, NDB, NVB)) void k_fused_s
     const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
     float xb[NDB][16], fb[NVB][16];
     auto load_x = [&](int t) {
-      ld_rows<T, NDB, FAST>(xb, rows_rsrc(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
+      ld_rows<T, NDB, FAST>(xb, rows_rsrc(x_b, x_sn, x_w, tile_p0(t, ntiles_, rev_), N), vrx, D, h);
     };
     auto load_f = [&](int t) {
-      const Rsrc rf = rows_rsrc(f_b, f_sn, f_w, (int64_t)t * kTile, N);
+      const Rsrc rf = rows_rsrc(f_b, f_sn, f_w, tile_p0(t, ntiles_, rev_), N);
 #pragma unroll
       for (int vb = 0; vb < NVB; ++vb) ld_cols_here<T>(fb[vb], rf, vcf[vb], (uint32_t)f_sn);
     };
@@ -287,11 +289,11 @@ __global__ __launch_bounds__(256, slice_fwd_waves(NGB, NDB, NVB)) void k_fused_s
     // its split (at C4's shape 0.826 -> 0.803 ms against reloading both
     // blocks after the last product, and no scratch in the tile loop)
     auto load_f1 = [&](int t, int vb) {
-      const Rsrc rf = rows_rsrc_sel(f_b, f_sn, f_w, (int64_t)t * kTile, N);
+      const Rsrc rf = rows_rsrc_sel(f_b, f_sn, f_w, tile_p0(t, ntiles_, rev_), N);
       ld_cols_here<T>(fb[vb], rf, vcf[vb], (uint32_t)f_sn);
     };
     auto body = [&](int t, auto par) {
-      const int64_t p0 = (int64_t)t * kTile;
+      const int64_t p0 = tile_p0(t, ntiles_, rev_);
       const bool pv = p0 + c < N;
       constexpr float sg = decltype(par)::sign;
       float t2[NGB][16], w[NGB][16], m2, lsum;
@@ -399,10 +401,10 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
     const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
     float xA[NDB][16], xB[NDB][16];
     auto load = [&](float (&xn)[NDB][16], int t) {
-      ld_rows<T, NDB, FAST>(xn, rows_rsrc(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
+      ld_rows<T, NDB, FAST>(xn, rows_rsrc(x_b, x_sn, x_w, tile_p0(t, ntiles_, rev_), N), vrx, D, h);
     };
     auto body = [&](const float (&xf)[NDB][16], int t, auto par) {
-      const int64_t p0 = (int64_t)t * kTile;
+      const int64_t p0 = tile_p0(t, ntiles_, rev_);
       const bool pv = p0 + c < N;
       float t2[NGB][16], w[NGB][16], m2, lsum;
       {
@@ -561,13 +563,13 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
     // buffer is reloaded for the wave's next tile right there
     float xA[NDB][16], xB[NDB][16], ff[NVB][16];
     auto load = [&](float (&xn)[NDB][16], int t) {
-      ld_rows<T, NDB, FAST>(xn, rows_rsrc_sel(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
+      ld_rows<T, NDB, FAST>(xn, rows_rsrc_sel(x_b, x_sn, x_w, tile_p0(t, ntiles_, rev_), N), vrx, D, h);
     };
     auto load_f = [&](int t) {
-      ld_rows<T, NVB, FAST>(ff, rows_rsrc_sel(f_b, f_sn, f_w, (int64_t)t * kTile, N), vrf, DV, h);
+      ld_rows<T, NVB, FAST>(ff, rows_rsrc_sel(f_b, f_sn, f_w, tile_p0(t, ntiles_, rev_), N), vrf, DV, h);
     };
     auto body = [&](const float (&xf)[NDB][16], int t, auto par) {
-      const int64_t p0 = (int64_t)t * kTile;
+      const int64_t p0 = tile_p0(t, ntiles_, rev_);
       const bool pv = p0 + c < N;
       constexpr float sg = decltype(par)::sign;
       float t2[NGB][16], w[NGB][16], m2, lsum;
@@ -754,13 +756,13 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
     // buffer is reloaded for the wave's next tile right there
     float xA[NDB][16], xB[NDB][16], of[NVB][16];
     auto load = [&](float (&xn)[NDB][16], int t) {
-      ld_rows<T, NDB, FAST>(xn, rows_rsrc_sel(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
+      ld_rows<T, NDB, FAST>(xn, rows_rsrc_sel(x_b, x_sn, x_w, tile_p0(t, ntiles_, rev_), N), vrx, D, h);
     };
     auto load_g = [&](int t) {
-      ld_rows<T, NVB, FAST>(of, rows_rsrc_sel(g_b, g_sn, g_w, (int64_t)t * kTile, N), vrg, DV, h);
+      ld_rows<T, NVB, FAST>(of, rows_rsrc_sel(g_b, g_sn, g_w, tile_p0(t, ntiles_, rev_), N), vrg, DV, h);
     };
     auto body = [&](const float (&xf)[NDB][16], int t, auto par) {
-      const int64_t p0 = (int64_t)t * kTile;
+      const int64_t p0 = tile_p0(t, ntiles_, rev_);
       const bool pv = p0 + c < N;
       constexpr float sg = decltype(par)::sign;
       float t2[NGB][16], w[NGB][16], m2, lsum;
@@ -985,16 +987,16 @@ __global__ __launch_bounds__(256, (NGB * NDB * NVB == 1) ? 2 : 1) void k_fused_t
     // once omega and d_out's transpose have consumed them
     float xA[NDB][16], xB[NDB][16], ff[NVB][16], of[NVB][16];
     auto load = [&](float (&xn)[NDB][16], int t) {
-      ld_rows<T, NDB, FAST>(xn, rows_rsrc_sel(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
+      ld_rows<T, NDB, FAST>(xn, rows_rsrc_sel(x_b, x_sn, x_w, tile_p0(t, ntiles_, rev_), N), vrx, D, h);
     };
     auto load_f = [&](int t) {
-      ld_rows<T, NVB, FAST>(ff, rows_rsrc_sel(f_b, f_sn, f_w, (int64_t)t * kTile, N), vrf, DV, h);
+      ld_rows<T, NVB, FAST>(ff, rows_rsrc_sel(f_b, f_sn, f_w, tile_p0(t, ntiles_, rev_), N), vrf, DV, h);
     };
     auto load_g = [&](int t) {
-      ld_rows<T, NVB, FAST>(of, rows_rsrc_sel(g_b, g_sn, g_w, (int64_t)t * kTile, N), vrg, DV, h);
+      ld_rows<T, NVB, FAST>(of, rows_rsrc_sel(g_b, g_sn, g_w, tile_p0(t, ntiles_, rev_), N), vrg, DV, h);
     };
     auto body = [&](const float (&xf)[NDB][16], int t, auto par) {
-      const int64_t p0 = (int64_t)t * kTile;
+      const int64_t p0 = tile_p0(t, ntiles_, rev_);
       const bool pv = p0 + c < N;
       constexpr float sg = decltype(par)::sign;
       float t2[NGB][16], w[NGB][16], m2, lsum;
@@ -1219,16 +1221,16 @@ __global__ __launch_bounds__(256, 2) void k_fused_tied_nodt(Args a) {
     // the wave's next tile as soon as each is split
     float xA[1][16], xB[1][16], ff[1][16], of[1][16];
     auto load = [&](float (&xn)[1][16], int t) {
-      ld_rows<T, 1, FAST>(xn, rows_rsrc_sel(x_b, x_sn, x_w, (int64_t)t * kTile, N), vrx, D, h);
+      ld_rows<T, 1, FAST>(xn, rows_rsrc_sel(x_b, x_sn, x_w, tile_p0(t, ntiles_, rev_), N), vrx, D, h);
     };
     auto load_f = [&](int t) {
-      ld_rows<T, 1, FAST>(ff, rows_rsrc_sel(f_b, f_sn, f_w, (int64_t)t * kTile, N), vrf, DV, h);
+      ld_rows<T, 1, FAST>(ff, rows_rsrc_sel(f_b, f_sn, f_w, tile_p0(t, ntiles_, rev_), N), vrf, DV, h);
     };
     auto load_g = [&](int t) {
-      ld_rows<T, 1, FAST>(of, rows_rsrc_sel(g_b, g_sn, g_w, (int64_t)t * kTile, N), vrg, DV, h);
+      ld_rows<T, 1, FAST>(of, rows_rsrc_sel(g_b, g_sn, g_w, tile_p0(t, ntiles_, rev_), N), vrg, DV, h);
     };
     auto body = [&](const float (&xf)[1][16], int t, auto par) {
-      const int64_t p0 = (int64_t)t * kTile;
+      const int64_t p0 = tile_p0(t, ntiles_, rev_);
       const bool pv = p0 + c < N;
       constexpr float sg = decltype(par)::sign;
       float t2[1][16], w[1][16], m2, lsum;

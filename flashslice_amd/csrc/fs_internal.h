@@ -37,6 +37,7 @@ struct Args {
   int B, N, H, D, DV, G;
   int P;                                   // point partitions per (b, h), a multiple of 4
   int no_dtok;                             // tied bwd: dtokens not asked for (not formed)
+  int rev;                                 // whole-G kernels: tiles visited last-first (tile_p0)
   int ntiles;                              // ceil(N / 32)
   int vec_x, vec_f, vec_1, vec_2;          // 4-element alignment of rows
   int fast;                                // all rows aligned, D and DV multiples of 32

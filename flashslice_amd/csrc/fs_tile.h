@@ -220,6 +220,19 @@ __device__ __forceinline__ void copy_frags(float (&dst)[NB][16], const float (&s
     for (int j = 0; j < 16; ++j) dst[k][j] = src[k][j];
 }
 
+// First point of the wave's tile t (of the sequence pid, pid + P, ... below
+// ntiles). With rev set the sequence covers the tiles last-first (tile t
+// holds the points of tile ntiles - 1 - t), and the whole-G prologue maps
+// the blocks to (b, h) pairs last-first as well: a grid that takes several
+// dispatch rounds streams its pairs in blockIdx.y order, so that a kernel
+// which follows one that swept in order starts on the pairs and points its
+// predecessor touched last, part of which the 256 MB last-level cache still
+// holds. An index at or past ntiles (a prefetch past the wave's last tile)
+// stays past the end.
+__device__ __forceinline__ int64_t tile_p0(int t, int ntiles, int rev) {
+  return (int64_t)(rev && t < ntiles ? ntiles - 1 - t : t) * kTile;
+}
+
 // Issue priority of a wave from its remaining tiles (after tile t of the
 // sequence pid, pid + P, ... below ntiles): the quarter of its work still
 // ahead of it, 3 (all of it) down to 0. Waves of one SIMD that share a
