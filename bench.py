@@ -38,6 +38,11 @@ the committed profiles/<workload>[-tied]_hbm_traffic.txt), ``step_roofline``
 oracle -- the eager PyTorch softmax/einsum path -- timed on a bounded sample
 on this host's cores), ``peak_hbm_gb``, ``per_op_ms``, ``deterministic`` and
 ``public_api`` (the same step through the public API and autograd).
+
+The timed steps carry one HIP event at each step boundary and a pair around
+the dominant op only; ``per_op_ms`` comes from K steps with events around
+every op, run before them (a timing event is a marker the GPU waits on:
+eight per step cost ~30 us of the C2 step).
 """
 
 import argparse
@@ -236,7 +241,7 @@ def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", dot=0
     given tokens are deslided, then the points are slided again (config 4's
     persistent point stream), and the backward runs in autograd's order
     (slice, then deslice). ``ev``: a (start, end) event pair per op name,
-    recorded around exactly that op. ``tied``: the backward as
+    recorded around exactly that op (ops it does not name run bare). ``tied``: the backward as
     ``fused_coupling`` runs it instead of the two backward ops (whose two dx
     autograd would still have to add): deslice-first the one tied operator
     (flashslice::deslice_slice_bwd, one pass for both ops' gradients and a
@@ -249,7 +254,7 @@ def step_ops(x, fx, W, b, tau, d_out, dzb, dsb, tok0, order="slice-first", dot=0
     from flashslice_amd.kernels.slice_ops import _whole_g, stats_placeholder
 
     def timed(name, fn, *args):
-        if ev is None:
+        if ev is None or name not in ev:
             return fn(*args)
         ev[name][0].record()
         r = fn(*args)
@@ -824,12 +829,13 @@ def main():
               flush=True)
         del probe
 
-    # the timed region's events, created (and recorded once) before any step:
-    # the host work of creating them then leaves no idle gap before the timed
-    # steps
-    pairs = iter(event_pairs(a.steps * (len(ops_timed) + 1)))
+    # every event of the measurement, created (and recorded once) before any
+    # step: the host work of creating them then leaves no idle gap before the
+    # timed steps
+    pairs = iter(event_pairs(a.steps * len(ops_timed)))
     evs = [{n: next(pairs) for n in ops_timed} for _ in range(a.steps)]
-    sev = [next(pairs) for _ in range(a.steps)]
+    bounds = timing_events(a.steps + 1)
+    dom_ev = event_pairs(a.steps)
     gc_quiet = quiet_gc()
     gc_quiet.__enter__()
 
@@ -848,58 +854,70 @@ def main():
     peak_gb = (torch.cuda.max_memory_allocated() - base) / 1e9
     del res
 
-    # timed region: K steps, per-op HIP events on the launch stream, right
-    # after the W warmup steps
+    # the per-op breakdown: K steps with HIP events around every op, after
+    # the W warmup steps. Each event is a marker in the stream that the GPU
+    # waits on (measured at C2: ~30 us per step for the eight), so the timed
+    # steps below carry only those the line needs.
     for _ in range(a.warmup):
         run_step()
+    for i in range(a.steps):
+        run_step(ev=evs[i])
+    torch.cuda.synchronize()
+    per_op = {n: sum(e[n][0].elapsed_time(e[n][1]) for e in evs) / a.steps for n in ops_timed}
+    dom = max(per_op, key=per_op.get)
+
+    # timed region: K steps; one HIP event at each step boundary and a pair
+    # around the dominant kernel (the roofline's launch duration, live)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    bounds[0].record()
     for i in range(a.steps):
-        sev[i][0].record()
-        run_step(ev=evs[i])
-        sev[i][1].record()
+        run_step(ev={dom: dom_ev[i]})
+        bounds[i + 1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    dom_ms = sum(e0.elapsed_time(e1) for e0, e1 in dom_ev) / a.steps
     # the other form of the backward where the whole-G kernels serve both
-    # (the two backward ops against the merged one), the same K steps after
-    # W warmup steps, HIP-event timed
+    # (the two backward ops against the merged one): its per-op breakdown,
+    # then K steps timed the same way, after W warmup steps
     alt = None
     if whole:
         alt_tied = not a.tied
         alt_ops = ops_of(alt_tied)
         run_alt = functools.partial(step_ops, *inputs, order=order, dot=dot, blocked=blocked,
                                     tied=alt_tied)
-        apairs = iter(event_pairs(a.steps * (len(alt_ops) + 1)))
+        apairs = iter(event_pairs(a.steps * len(alt_ops)))
         aevs = [{n: next(apairs) for n in alt_ops} for _ in range(a.steps)]
-        asev = [next(apairs) for _ in range(a.steps)]
+        abounds = timing_events(a.steps + 1)
         for _ in range(a.warmup):
             run_alt()
         for i in range(a.steps):
-            asev[i][0].record()
             run_alt(ev=aevs[i])
-            asev[i][1].record()
+        abounds[0].record()
+        for i in range(a.steps):
+            run_alt()
+            abounds[i + 1].record()
         torch.cuda.synchronize()
-        ams = sorted(e0.elapsed_time(e1) for e0, e1 in asev)
+        ams = sorted(abounds[i].elapsed_time(abounds[i + 1]) for i in range(a.steps))
         alt = {"backward": "tied" if alt_tied else "two ops",
                "ms_per_step_median": round(ams[len(ams) // 2], 4),
                "per_op_ms": {n: round(sum(e[n][0].elapsed_time(e[n][1]) for e in aevs)
                                       / a.steps, 4) for n in alt_ops}}
     gc_quiet.__exit__(None, None, None)
     ms_step = 1e3 * wall / a.steps
-    step_ms = sorted(e0.elapsed_time(e1) for e0, e1 in sev)
+    in_order = [bounds[i].elapsed_time(bounds[i + 1]) for i in range(a.steps)]
+    step_ms = sorted(in_order)
     ms_median = step_ms[len(step_ms) // 2]
     print("[bench] event-timed steps: min %.4f median %.4f max %.4f ms; wall mean %.4f ms; "
           "in order: %s" % (step_ms[0], ms_median, step_ms[-1], 1e3 * wall / a.steps,
-                            " ".join("%.3f" % e0.elapsed_time(e1) for e0, e1 in sev)),
+                            " ".join("%.3f" % t for t in in_order)),
           file=sys.stderr, flush=True)
-    per_op = {n: sum(e[n][0].elapsed_time(e[n][1]) for e in evs) / a.steps for n in ops_timed}
     bytes_ = alg_bytes(B, N, H, D, DV, 2 if a.dot == "bf16" else 4)
     flops = alg_flops(B, N, H, D, DV, G)
     if order == "slice-first":
         flops["tied_bwd"] = flops.pop("tied_bwd_sf")
-    dom = max(per_op, key=per_op.get)
-    ach = bytes_[dom] / (per_op[dom] * 1e-3) / 1e9
-    ach_tf = flops[dom] / (per_op[dom] * 1e-3) / 1e12
+    ach = bytes_[dom] / (dom_ms * 1e-3) / 1e9
+    ach_tf = flops[dom] / (dom_ms * 1e-3) / 1e12
     # the step's algorithmic units are the four ops' (the metric's unit),
     # whichever form the backward takes
     total_bytes = sum(bytes_[n] for n in OPS)
@@ -955,6 +973,9 @@ def main():
                           "alg_flops": total_flops,
                           "alg_tflops": round(total_flops / (ms_step * 1e-3) / 1e12, 2)},
         "per_op_ms": {k: round(v, 4) for k, v in per_op.items()},
+        "per_op_source": "K steps with HIP events around every op, before the timed steps "
+                         "(which carry events only at step boundaries and around the "
+                         "dominant kernel)",
         "peak_hbm_gb": round(peak_gb, 3),
         "nxhxg_gb": round(B * N * H * G * 4 / 1e9, 3),
         "deterministic": deterministic,
@@ -965,7 +986,7 @@ def main():
     line["roofline"].update({
         "traffic": traffic.get(dom) if traffic else None,
         "alg_bytes_per_launch": bytes_[dom], "alg_flops_per_launch": flops[dom],
-        "ms_per_launch": round(per_op[dom], 4)})
+        "ms_per_launch": round(dom_ms, 4)})
     print(json.dumps(line), flush=True)
 
 
