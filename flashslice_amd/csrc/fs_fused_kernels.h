@@ -269,10 +269,10 @@ __global__ __launch_bounds__(256, slice_fwd_waves(NGB, NDB, NVB)) void k_fused_s
     FS_TILE_LOOP_LOADED(load, body, true, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
   };
   // The wider shapes: one buffer per point stream, each reloaded for the
-  // wave's next tile right after its last use (x after the logits, fx once
-  // split, after the softmax): 349 registers instead of 393 at C4's shape,
-  // still one wave per SIMD, 4 % faster there (1.009 against 1.053 ms; fitted
-  // to 256 registers for two waves it spills and takes 1.93 ms).
+  // wave's next tile right after its last use (x after the logits, each
+  // value block of fx right after its split), and w's split pieces held for
+  // all slot blocks while fx's are held for one value block: 254 registers
+  // without spills at C4's shape, two waves per SIMD.
   auto run_wide = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
     const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
