@@ -16,8 +16,9 @@
 // per (point, slot), and each point tile is read from HBM once.
 //
 // Each point tile is loaded once per block: 256 threads load it (16 bytes
-// each) while the previous tile is computed and store it in LDS as bf16 rows
-// in the transposable layout of tr_put, three buffers deep; the waves read
+// each; two tiles ahead in the forward kernels, one in the backward) and
+// store it in LDS as bf16 rows in the transposable layout of tr_put, three
+// buffers deep; the waves read
 // their MFMA operands from there, plain ([point, column]) or transposed
 // (ds_read_b64_tr_b16), with no fp32 round trip. Per tile, a slice forward
 // waits at one block barrier (the next tile and, without statistics, the
@@ -25,6 +26,7 @@
 // dx / dfx exchange). The tile loop is identical in every wave of a block,
 // so the barriers are uniform.
 #pragma once
+#include <type_traits>
 #include "fs_device.h"
 #include "fs_internal.h"
 #include "fs_io.h"
@@ -201,30 +203,88 @@ __device__ __forceinline__ void tile_rows(Frag<MMA_BF16>& f, const char* region,
 }
 
 // Staging of the block's point tiles: threads 0..127 take x, 128..255 the
-// second stream (fx or d_out; TWO = false: none); three LDS buffers rotate,
-// so the tile stored for the next step never overwrites one a slower wave
-// may still read.
-#define COOP_STAGING(FAST, TWO)                                                         \
+// second stream (fx or d_out; TWO = false: none), each 16 bytes of a tile
+// into a ring of DEPTH register sets, tiles t, t + P, ... in order; a tile
+// is published from its set into one of three rotating LDS buffers (so the
+// tile stored for the next step never overwrites one a slower wave may still
+// read), and the set is refilled with the tile DEPTH steps later. Set
+// indices are compile-time (the tile loop is unrolled over the ring). Waves
+// that stage nothing issue the same loads on an empty range (zeros, no
+// memory traffic): every wave then has the same loads outstanding, and the
+// compiler waits at a publish for that one tile, not for all of them.
+#define COOP_STAGING(FAST, TWO, DEPTH)                                                  \
   /* waves 0, 1 load x, waves 2, 3 the second stream: conditions on the   */           \
   /* (scalar) wave index, so each load sees one uniform buffer resource   */           \
   const int li_ = ((wid & 1) << 6) | lane;                                              \
   const bool ldx_ = wid < 2, ldf_ = (TWO) && wid >= 2 && wid < 4;                       \
-  uint32_t stg_[4] = {0u, 0u, 0u, 0u};                                                  \
+  uint32_t stg_[DEPTH][4];                                                              \
+  _Pragma("unroll") for (int s_ = 0; s_ < (DEPTH); ++s_)                                \
+    _Pragma("unroll") for (int e_ = 0; e_ < 4; ++e_) stg_[s_][e_] = 0u;                 \
   /* the block's tiles in order: pid, pid + P, ... (one cursor per wave) */             \
   TileCursor gk_ = ldx_ ? tile_cursor(x_b, x_sn, x_w, pid, a.P, N)                      \
                         : tile_cursor(f_b, f_sn, f_w, pid, a.P, N);                     \
   const int64_t gsn_ = ldx_ ? x_sn : f_sn;                                              \
   const int gC_ = ldx_ ? D : DV;                                                        \
-  auto gload = [&]() {                                                                  \
-    if (ldx_ || ldf_) coop_tile_load<T, FAST>(stg_, gk_.rsrc(), gsn_, gC_, li_);        \
+  auto gload = [&](auto s_c) {                                                          \
+    constexpr int s = decltype(s_c)::value;                                             \
+    const Rsrc r_ = (ldx_ || ldf_) ? gk_.rsrc()                                         \
+                                   : __builtin_amdgcn_make_buffer_rsrc(                 \
+                                         const_cast<char*>(x_b), (short)0, 0, kRsrcWord3); \
+    coop_tile_load<T, FAST>(stg_[s], r_, gsn_, gC_, li_);                               \
     gk_.next();                                                                         \
   };                                                                                    \
   auto tile_at = [&](int buf, int stream) -> char* {                                    \
     return tiles_ + (2 * buf + stream) * kCoopTileB;                                    \
   };                                                                                    \
-  auto lstore = [&](int buf) {                                                          \
-    if (ldx_ || ldf_) coop_tile_store(tile_at(buf, ldx_ ? 0 : 1), stg_, li_);           \
+  auto lstore = [&](int buf, auto s_c) {                                                \
+    constexpr int s = decltype(s_c)::value;                                             \
+    if (ldx_ || ldf_) coop_tile_store(tile_at(buf, ldx_ ? 0 : 1), stg_[s], li_);        \
   };
+template <int V> using IC = std::integral_constant<int, V>;
+// Tiles in flight per block: two for the forward kernels (at config 3's
+// G = 256 with bf16 dots the slice forward 0.952 -> 0.918 ms, the deslice
+// forward 0.652 -> 0.609 ms against one); one for the backward, which two
+// did not speed up (1.66 ms either way: it is bound by its two barriers and
+// its LDS traffic per tile).
+constexpr int kCoopDepthFwd = 2, kCoopDepthBwd = 1;
+
+// The tile loop of a block-cooperative kernel: the first DEPTH tiles
+// staged and the first one published (PRE: what else the first tile needs
+// before the first barrier), then BODY(t, LDS buffer, parity, ring set to
+// publish and refill) per tile, unrolled over the ring and the parity.
+#define COOP_TILE_LOOP(DEPTH, BODY, PRE)                                                \
+  {                                                                                     \
+    int t = pid, cur = 0;                                                               \
+    constexpr int DP = (DEPTH);                                                         \
+    static_assert(DP == 1 || DP == 2 || DP == 4, "staging depth 1, 2 or 4");           \
+    gload(IC<0>());                                                                     \
+    if constexpr (DP > 1) gload(IC<1 % DP>());                                          \
+    if constexpr (DP > 2) {                                                             \
+      gload(IC<2 % DP>());                                                              \
+      gload(IC<3 % DP>());                                                              \
+    }                                                                                   \
+    lstore(0, IC<0>());                                                                 \
+    gload(IC<0>()); /* tile DP */                                                       \
+    PRE;                                                                                \
+    __syncthreads();                                                                    \
+    auto adv_ = [&]() {                                                                 \
+      t += a.P;                                                                         \
+      cur = cur == 2 ? 0 : cur + 1;                                                     \
+      return t < ntiles_;                                                               \
+    };                                                                                  \
+    while (t < ntiles_) {                                                               \
+      BODY(t, cur, TileEven(), IC<1 % DP>());                                           \
+      if (!adv_()) break;                                                               \
+      BODY(t, cur, TileOdd(), IC<2 % DP>());                                            \
+      if (!adv_()) break;                                                               \
+      if constexpr (DP > 2) {                                                           \
+        BODY(t, cur, TileEven(), IC<3 % DP>());                                         \
+        if (!adv_()) break;                                                             \
+        BODY(t, cur, TileOdd(), IC<4 % DP>());                                          \
+        if (!adv_()) break;                                                             \
+      }                                                                                 \
+    }                                                                                   \
+  }
 
 // ------------------------------------------------------------------ slice fwd
 // z_num, s of the wave's slots. Exponentials against the wave's own row max;
@@ -247,13 +307,14 @@ __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
   const float* sm = a.stats_in ? a.stats_in + R_.stats_off() : nullptr;
   const float* st_m = a.stats_out ? a.stats_out + R_.stats_off() : nullptr;
   const float* st_l = st_m ? st_m + R_.NS : nullptr;
-  auto run = [&](auto fast_c) {
+  auto run = [&](auto fast_c, auto sm_c) {
     constexpr bool FAST = decltype(fast_c)::value;
-    COOP_STAGING(FAST, true)
+    constexpr bool SM = decltype(sm_c)::value;  // saved statistics read
+    COOP_STAGING(FAST, true, kCoopDepthFwd)
     // per-point statistics of the block's tiles, in order (read or written)
     TileCursor km = tile_cursor(sm ? sm : st_m, 4, 4, pid, a.P, (sm || st_m) ? N : 0);
     TileCursor kl = tile_cursor(sm ? sm + R_.NS : st_l, 4, 4, pid, a.P, (sm || st_m) ? N : 0);
-    auto body = [&](int t, int cur, auto par) {
+    auto body = [&](int t, int cur, auto par, auto slot) {
       const bool pv = t * kTile + c < N;
       constexpr float sg = decltype(par)::sign;
       Frag<M> xq;
@@ -271,18 +332,18 @@ __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
         ls += e[r];
       }
       float* xb = xpt + (sg < 0.f ? 2 * kCoopWaves * 32 : 0);
-      if (!sm) {
+      if constexpr (!SM) {
         ls = pair_sum(ls);
         if (h == 0) {
           xb[wid * 32 + c] = m;
           xb[kCoopWaves * 32 + wid * 32 + c] = ls;
         }
       }
-      lstore(cur == 2 ? 0 : cur + 1);  // publish the next tile
+      lstore(cur == 2 ? 0 : cur + 1, slot);  // publish the next tile
       __syncthreads();
-      gload();  // the tile after it (t + 2 P), into the staging registers
+      gload(slot);  // tile t + (1 + depth) P into the set just published
       float m2, l;
-      if (sm) {
+      if constexpr (SM) {
         m2 = ld_pt(km.rsrc(), c) * kLog2e;
         l = ld_pt(kl.rsrc(), c);
       } else {
@@ -315,22 +376,13 @@ __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
       tr_get<M>(fT, tile_at(cur, 1), lane);
       zacc = mma<M>(fT, wTq, zacc);
     };
-    int t = pid, cur = 0;
-    gload();  // t
-    lstore(0);
-    gload();  // t + P
-    __syncthreads();
-    while (t < ntiles_) {
-      body(t, cur, TileEven());
-      t += a.P;
-      cur = cur == 2 ? 0 : cur + 1;
-      if (t >= ntiles_) break;
-      body(t, cur, TileOdd());
-      t += a.P;
-      cur = cur == 2 ? 0 : cur + 1;
-    }
+    COOP_TILE_LOOP(kCoopDepthFwd, body, (void)0)
   };
-  if (fast) run(std::true_type()); else run(std::false_type());
+  if (sm) {
+    if (fast) run(std::true_type(), std::true_type()); else run(std::false_type(), std::true_type());
+  } else {
+    if (fast) run(std::true_type(), std::false_type()); else run(std::false_type(), std::false_type());
+  }
   // the block's partial: the wave's slots of z_num (rows g0 + c) and s
   const int64_t E = part_floats_slice_fwd(G, DV);
   float* pw = a.part + ((int64_t)bh * gridDim.x + blockIdx.x) * E;
@@ -402,9 +454,11 @@ __device__ __forceinline__ void ps_operand(bf16x8 (&A)[kCoopWaves], const float*
 // columns of one point per lane. With saved statistics w = exp2(t2 - (m2 +
 // log2 l)) and one barrier per tile; without, the waves' (max, sum) pairs
 // are combined after a first barrier (as in the slice forward) and written
-// to stats_out when asked for.
+// to stats_out when asked for. Compiled for four waves per SIMD (128
+// registers; its 68 KB of LDS fits two blocks per CU, which the two staged
+// tiles would otherwise cost at 129).
 template <typename T>
-__global__ __launch_bounds__(kCoopThreads, 2) void k_coop_deslice_fwd(Args a) {
+__global__ __launch_bounds__(kCoopThreads, 4) void k_coop_deslice_fwd(Args a) {
   COOP_PROLOGUE(kCoopWRegFwd)
   const int ph = (wid >> 1) & 1, dh = wid & 1;
   const bool out_ = wid < 4;
@@ -420,9 +474,10 @@ __global__ __launch_bounds__(kCoopThreads, 2) void k_coop_deslice_fwd(Args a) {
   const float* sm = a.stats_in ? a.stats_in + R_.stats_off() : nullptr;
   const float* st_m = a.stats_out ? a.stats_out + R_.stats_off() : nullptr;
   const int op = 16 * ph + l16, oc = 16 * dh + 4 * kg;
-  auto run = [&](auto fast_c) {
+  auto run = [&](auto fast_c, auto sm_c) {
     constexpr bool FAST = decltype(fast_c)::value;
-    COOP_STAGING(FAST, false)
+    constexpr bool SM = decltype(sm_c)::value;  // saved statistics read
+    COOP_STAGING(FAST, false, kCoopDepthFwd)
     // statistics (saved ones, read one tile ahead; or computed ones,
     // written by wave 0) and out, the block's tiles in order
     const float* srow = sm ? sm : st_m;
@@ -437,7 +492,7 @@ __global__ __launch_bounds__(kCoopThreads, 2) void k_coop_deslice_fwd(Args a) {
       km.next();
       kl.next();
     };
-    auto body = [&](int t, int cur, auto par) {
+    auto body = [&](int t, int cur, auto par, auto slot) {
       const bool pv = t * kTile + c < N;
       constexpr float sg = decltype(par)::sign;
       constexpr int q = sg < 0.f ? 1 : 0;
@@ -446,12 +501,12 @@ __global__ __launch_bounds__(kCoopThreads, 2) void k_coop_deslice_fwd(Args a) {
       tile_rows(xq, tile_at(cur, 0), c, h);
       float t2[16], w[16];
       COOP_LOGITS(t2, xq)
-      if (sm) {
+      if constexpr (SM) {
         const float sh = pv ? fmaf(smv[q], kLog2e, __builtin_amdgcn_logf(slv[q])) : kFarShift;
         sload(q ^ 1);  // t + P
 #pragma unroll
         for (int r = 0; r < 16; ++r) w[r] = __builtin_amdgcn_exp2f(t2[r] - sh);
-        lstore(cur == 2 ? 0 : cur + 1);  // publish the next tile
+        lstore(cur == 2 ? 0 : cur + 1, slot);  // publish the next tile
       } else {
         float m = -INFINITY;
 #pragma unroll
@@ -469,7 +524,7 @@ __global__ __launch_bounds__(kCoopThreads, 2) void k_coop_deslice_fwd(Args a) {
           xb[wid * 32 + c] = m;
           xb[kCoopWaves * 32 + wid * 32 + c] = ls;
         }
-        lstore(cur == 2 ? 0 : cur + 1);  // publish the next tile
+        lstore(cur == 2 ? 0 : cur + 1, slot);  // publish the next tile
         __syncthreads();
         float m2 = xb[c];
 #pragma unroll
@@ -489,7 +544,7 @@ __global__ __launch_bounds__(kCoopThreads, 2) void k_coop_deslice_fwd(Args a) {
       prep<M>(wq, w);
       ps_put(wb, wq, wid, c, h);
       __syncthreads();
-      gload();  // t + 2 P
+      gload(slot);  // tile t + (1 + depth) P into the set just published
       const Rsrc ro = ko.rsrc();
       ko.next();
       if (out_) {
@@ -503,23 +558,13 @@ __global__ __launch_bounds__(kCoopThreads, 2) void k_coop_deslice_fwd(Args a) {
         }
       }
     };
-    int t = pid, cur = 0;
-    gload();  // t
-    lstore(0);
-    gload();  // t + P
-    if (sm) sload(0);  // t
-    __syncthreads();
-    while (t < ntiles_) {
-      body(t, cur, TileEven());
-      t += a.P;
-      cur = cur == 2 ? 0 : cur + 1;
-      if (t >= ntiles_) break;
-      body(t, cur, TileOdd());
-      t += a.P;
-      cur = cur == 2 ? 0 : cur + 1;
-    }
+    COOP_TILE_LOOP(kCoopDepthFwd, body, if constexpr (SM) sload(0))
   };
-  if (fast) run(std::true_type()); else run(std::false_type());
+  if (sm) {
+    if (fast) run(std::true_type(), std::true_type()); else run(std::false_type(), std::true_type());
+  } else {
+    if (fast) run(std::true_type(), std::false_type()); else run(std::false_type(), std::false_type());
+  }
 }
 
 // ---------------------------------------------------------------- backward
@@ -582,7 +627,7 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
   const int oC = os == 0 ? D : DV;
   auto run = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
-    COOP_STAGING(FAST, true)
+    COOP_STAGING(FAST, true, kCoopDepthBwd)
     // the statistics of a wave's tiles, loaded one tile ahead (a load waited
     // for in the same tile would expose a whole memory latency per tile);
     // [parity]: the even / odd bodies of the unrolled loop
@@ -598,7 +643,7 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
                             : tile_cursor(df_b, df_sn, df_w, pid, a.P, N);
     const int64_t osn = os == 0 ? dx_sn : df_sn;
     const uint32_t ooff = (uint32_t)(op * osn) + (uint32_t)(oc * (int)sizeof(T));
-    auto body = [&](int t, int cur, auto par) {
+    auto body = [&](int t, int cur, auto par, auto slot) {
       const bool pv = t * kTile + c < N;
       constexpr int q = decltype(par)::sign < 0.f ? 1 : 0;
       Frag<M> xq, fq;
@@ -639,9 +684,9 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
         tr_get<M>(wTq, trB, lane);
         dT = mma<M>(oTq, wTq, dT);
       }
-      lstore(cur == 2 ? 0 : cur + 1);  // publish the next tile
+      lstore(cur == 2 ? 0 : cur + 1, slot);  // publish the next tile
       __syncthreads();
-      gload();  // t + 2 P
+      gload(slot);  // tile t + (1 + depth) P into the set just published
       float delta = 0.f;
 #pragma unroll
       for (int wv = 0; wv < kCoopWaves; ++wv) delta += xpt[wv * 32 + c];
@@ -684,21 +729,7 @@ __global__ __launch_bounds__(kCoopThreads, 1) void k_coop_bwd(Args a) {
         }
       }
     };
-    int t = pid, cur = 0;
-    gload();  // t
-    lstore(0);
-    gload();  // t + P
-    sload(0);  // t
-    __syncthreads();
-    while (t < ntiles_) {
-      body(t, cur, TileEven());
-      t += a.P;
-      cur = cur == 2 ? 0 : cur + 1;
-      if (t >= ntiles_) break;
-      body(t, cur, TileOdd());
-      t += a.P;
-      cur = cur == 2 ? 0 : cur + 1;
-    }
+    COOP_TILE_LOOP(kCoopDepthBwd, body, sload(0))
   };
   if (fast) run(std::true_type()); else run(std::false_type());
   // the block's partial: dW, db (and dtokens) of the wave's slots; dtau of
