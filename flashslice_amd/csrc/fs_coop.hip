@@ -8,10 +8,16 @@ template <typename T>
 static hipError_t coop_dispatch(int kind, const Args& a, hipStream_t st) {
   const dim3 grid(a.P, a.B * a.H), blk(kCoopThreads);
   switch (kind) {
-    case CK_SLICE_FWD: hipLaunchKernelGGL(k_coop_slice_fwd<T>, grid, blk, 0, st, a); break;
+    case CK_SLICE_FWD:
+      if (a.stats_in) hipLaunchKernelGGL((k_coop_slice_fwd<T, true>), grid, blk, 0, st, a);
+      else hipLaunchKernelGGL((k_coop_slice_fwd<T, false>), grid, blk, 0, st, a);
+      break;
     case CK_SLICE_BWD: hipLaunchKernelGGL((k_coop_bwd<T, true>), grid, blk, 0, st, a); break;
     case CK_DESLICE_BWD: hipLaunchKernelGGL((k_coop_bwd<T, false>), grid, blk, 0, st, a); break;
-    case CK_DESLICE_FWD: hipLaunchKernelGGL(k_coop_deslice_fwd<T>, grid, blk, 0, st, a); break;
+    case CK_DESLICE_FWD:
+      if (a.stats_in) hipLaunchKernelGGL((k_coop_deslice_fwd<T, true>), grid, blk, 0, st, a);
+      else hipLaunchKernelGGL((k_coop_deslice_fwd<T, false>), grid, blk, 0, st, a);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -293,7 +293,7 @@ constexpr int kCoopDepthFwd = 2, kCoopDepthBwd = 1;
 // (buffers alternate by tile parity, so a wave may write the next tile's
 // pair while another still reads this one's) and written to stats_out when
 // asked for.
-template <typename T>
+template <typename T, bool SM_>
 __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
   COOP_PROLOGUE(kCoopWRegFwd)
   __syncthreads();  // the staging area becomes the transpose region
@@ -311,9 +311,19 @@ __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
     constexpr bool FAST = decltype(fast_c)::value;
     constexpr bool SM = decltype(sm_c)::value;  // saved statistics read
     COOP_STAGING(FAST, true, kCoopDepthFwd)
-    // per-point statistics of the block's tiles, in order (read or written)
+    // per-point statistics of the block's tiles, in order: saved ones read
+    // one tile ahead (smv / slv by tile parity; a load waited for in its own
+    // tile would expose a whole memory latency per tile), or formed ones
+    // written by wave 0
     TileCursor km = tile_cursor(sm ? sm : st_m, 4, 4, pid, a.P, (sm || st_m) ? N : 0);
     TileCursor kl = tile_cursor(sm ? sm + R_.NS : st_l, 4, 4, pid, a.P, (sm || st_m) ? N : 0);
+    float smv[2] = {0.f, 0.f}, slv[2] = {1.f, 1.f};
+    auto sload = [&](int q) {
+      smv[q] = ld_pt(km.rsrc(), c);
+      slv[q] = ld_pt(kl.rsrc(), c);
+      km.next();
+      kl.next();
+    };
     auto body = [&](int t, int cur, auto par, auto slot) {
       const bool pv = t * kTile + c < N;
       constexpr float sg = decltype(par)::sign;
@@ -321,18 +331,28 @@ __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
       tile_rows(xq, tile_at(cur, 0), c, h);
       float t2[16];
       COOP_LOGITS(t2, xq)
-      float m = -INFINITY;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) m = fmaxf(m, t2[r]);
-      m = pair_max(m);
-      float e[16], ls = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        e[r] = __builtin_amdgcn_exp2f(t2[r] - m);
-        ls += e[r];
-      }
+      float w[16];
+      float m = 0.f;
       float* xb = xpt + (sg < 0.f ? 2 * kCoopWaves * 32 : 0);
-      if constexpr (!SM) {
+      if constexpr (SM) {
+        // w = exp2(t2 - m2) / l = exp2(t2 - sh), sh = m2 + log2 l (the
+        // saved l >= 1); points beyond N get sh = kFarShift, hence w = 0
+        constexpr int q = sg < 0.f ? 1 : 0;
+        const float sh = pv ? fmaf(smv[q], kLog2e, __builtin_amdgcn_logf(slv[q])) : kFarShift;
+        sload(q ^ 1);  // t + P
+#pragma unroll
+        for (int r = 0; r < 16; ++r) w[r] = __builtin_amdgcn_exp2f(t2[r] - sh);
+      } else {
+        m = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m = fmaxf(m, t2[r]);
+        m = pair_max(m);
+        float ls = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          w[r] = __builtin_amdgcn_exp2f(t2[r] - m);
+          ls += w[r];
+        }
         ls = pair_sum(ls);
         if (h == 0) {
           xb[wid * 32 + c] = m;
@@ -342,30 +362,24 @@ __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
       lstore(cur == 2 ? 0 : cur + 1, slot);  // publish the next tile
       __syncthreads();
       gload(slot);  // tile t + (1 + depth) P into the set just published
-      float m2, l;
-      if constexpr (SM) {
-        m2 = ld_pt(km.rsrc(), c) * kLog2e;
-        l = ld_pt(kl.rsrc(), c);
-      } else {
-        m2 = xb[c];
+      if constexpr (!SM) {
+        float m2 = xb[c];
 #pragma unroll
-        for (int w = 1; w < kCoopWaves; ++w) m2 = fmaxf(m2, xb[w * 32 + c]);
-        l = 0.f;
+        for (int w_ = 1; w_ < kCoopWaves; ++w_) m2 = fmaxf(m2, xb[w_ * 32 + c]);
+        float l = 0.f;
 #pragma unroll
-        for (int w = 0; w < kCoopWaves; ++w)
-          l += xb[kCoopWaves * 32 + w * 32 + c] * __builtin_amdgcn_exp2f(xb[w * 32 + c] - m2);
+        for (int w_ = 0; w_ < kCoopWaves; ++w_)
+          l += xb[kCoopWaves * 32 + w_ * 32 + c] * __builtin_amdgcn_exp2f(xb[w_ * 32 + c] - m2);
         if (wid == 0 && st_m) store_stats_at(km.rsrc(), kl.rsrc(), c, h, m2, l);
-      }
-      km.next();
-      kl.next();
-      // w = exp2(t2 - m) exp2(m - m2) / l
-      const float inv = pv ? __builtin_amdgcn_exp2f(m - m2) * __builtin_amdgcn_rcpf(l) : 0.f;
-      float w[16];
+        km.next();
+        kl.next();
+        // w = exp2(t2 - m) exp2(m - m2) / l
+        const float inv = pv ? __builtin_amdgcn_exp2f(m - m2) * __builtin_amdgcn_rcpf(l) : 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        w[r] = e[r] * inv;
-        sacc[r] += w[r];
+        for (int r = 0; r < 16; ++r) w[r] *= inv;
       }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[r] += w[r];
       // z_num += w^T fx: w read back transposed, fx^T straight from the
       // staged tile, chained through the accumulator (the sign alternation
       // of the fp32-accurate kernels, acc_add, is below bf16's resolution)
@@ -376,13 +390,12 @@ __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_slice_fwd(Args a) {
       tr_get<M>(fT, tile_at(cur, 1), lane);
       zacc = mma<M>(fT, wTq, zacc);
     };
-    COOP_TILE_LOOP(kCoopDepthFwd, body, (void)0)
+    COOP_TILE_LOOP(kCoopDepthFwd, body, if constexpr (SM) sload(0))
   };
-  if (sm) {
-    if (fast) run(std::true_type(), std::true_type()); else run(std::false_type(), std::true_type());
-  } else {
-    if (fast) run(std::true_type(), std::false_type()); else run(std::false_type(), std::false_type());
-  }
+  // saved statistics read (a.stats_in non-null): a compile-time case of
+  // the kernel, so that each case gets its own register allocation
+  using SMc = std::integral_constant<bool, SM_>;
+  if (fast) run(std::true_type(), SMc()); else run(std::false_type(), SMc());
   // the block's partial: the wave's slots of z_num (rows g0 + c) and s
   const int64_t E = part_floats_slice_fwd(G, DV);
   float* pw = a.part + ((int64_t)bh * gridDim.x + blockIdx.x) * E;
@@ -457,7 +470,7 @@ __device__ __forceinline__ void ps_operand(bf16x8 (&A)[kCoopWaves], const float*
 // to stats_out when asked for. Compiled for four waves per SIMD (128
 // registers; its 68 KB of LDS fits two blocks per CU, which the two staged
 // tiles would otherwise cost at 129).
-template <typename T>
+template <typename T, bool SM_>
 __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_deslice_fwd(Args a) {
   COOP_PROLOGUE(kCoopWRegFwd)
   const int ph = (wid >> 1) & 1, dh = wid & 1;
@@ -560,11 +573,10 @@ __global__ __launch_bounds__(kCoopThreads, 4) void k_coop_deslice_fwd(Args a) {
     };
     COOP_TILE_LOOP(kCoopDepthFwd, body, if constexpr (SM) sload(0))
   };
-  if (sm) {
-    if (fast) run(std::true_type(), std::true_type()); else run(std::false_type(), std::true_type());
-  } else {
-    if (fast) run(std::true_type(), std::false_type()); else run(std::false_type(), std::false_type());
-  }
+  // saved statistics read (a.stats_in non-null): a compile-time case of
+  // the kernel, so that each case gets its own register allocation
+  using SMc = std::integral_constant<bool, SM_>;
+  if (fast) run(std::true_type(), SMc()); else run(std::false_type(), SMc());
 }
 
 // ---------------------------------------------------------------- backward
