@@ -433,19 +433,27 @@ __global__ __launch_bounds__(256, NB == 1 ? 3 : 1) void k_gp_slice_g(Args a) {
   auto run = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
     const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
-    float xA[NB][16], xB[NB][16], fA[NB][16], fB[NB][16];
-    auto load = [&](float (&xn)[NB][16], float (&fn)[NB][16], int t) {
+    // a tile's statistics (m, l) travel with its rows in the register set,
+    // loaded two tiles ahead: a load issued and waited for in the tile's own
+    // body would be the youngest outstanding, and waiting for it would wait
+    // for the prefetched tiles too (config 3's slice forward: 3.44 -> 3.26
+    // ms at G = 256, 12.7 -> 11.9 at G = 1024, 7.5 -> 7.3 with bf16 dots)
+    float xA[NB][16], xB[NB][16], fA[NB][16], fB[NB][16], sA[2], sB[2];
+    auto load = [&](float (&xn)[NB][16], float (&fn)[NB][16], float (&sn)[2], int t) {
       const int64_t p0 = (int64_t)t * kTile;
       ld_rows<T, NB, FAST>(xn, rows_rsrc(x_b, x_sn, x_w, p0, N), vrx, D, h);
       const Rsrc rf = rows_rsrc(f_b, f_sn, f_w, p0, N);
 #pragma unroll
       for (int k = 0; k < NB; ++k) ld_cols<T>(fn[k], rf, vcf[k], (uint32_t)f_sn);
+      sn[0] = ld_pt(pts_rsrc(sm, p0, N), c);
+      sn[1] = ld_pt(pts_rsrc(sm + R_.NS, p0, N), c);
     };
-    auto body = [&](const float (&xf)[NB][16], const float (&fT)[NB][16], int t, auto par) {
+    auto body = [&](const float (&xf)[NB][16], const float (&fT)[NB][16], const float (&sv)[2],
+                    int t, auto par) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
-      const float m2 = ld_pt(pts_rsrc(sm, p0, N), c) * kLog2e;
-      const float l = ld_pt(pts_rsrc(sm + R_.NS, p0, N), c);
+      const float m2 = sv[0] * kLog2e;
+      const float l = sv[1];
       Frag<ML> xq[NB];
 #pragma unroll
       for (int k = 0; k < NB; ++k) prep<ML>(xq[k], xf[k]);
@@ -472,7 +480,7 @@ __global__ __launch_bounds__(256, NB == 1 ? 3 : 1) void k_gp_slice_g(Args a) {
       for (int j = 0; j < 16; ++j) s += wT[j];
       sacc = fmaf(s, sg, sacc);
     };
-    FS_TILE_LOOP(load, body, false, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
+    FS_TILE_LOOP(load, body, false, FS_ARGS3(xA, fA, sA), FS_ARGS3(xB, fB, sB))
   };
   if (fast) run(std::true_type()); else run(std::false_type());
   float* pw = a.part + ((int64_t)bh * P + pid) * part_floats_slice_fwd(G, DV);
@@ -725,18 +733,31 @@ __global__ __launch_bounds__(256, NB == 1 && SLICE ? 3 : gp_waves(NB)) void k_gp
     constexpr bool FAST = decltype(fast_c)::value;
     const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
     const uint32_t vrf = FAST ? f_row + 4 * h * (uint32_t)sizeof(T) : f_row;
-    float xA[NB][16], xB[NB][16], fA[NB][16], fB[NB][16];
-    auto load = [&](float (&xn)[NB][16], float (&fn)[NB][16], int t) {
+    // with the value operands split (the fp32-accurate levels), a tile's
+    // per-point values (m, l, delta) travel with its rows in the register
+    // set, loaded two tiles ahead as in the slot-owned slice (config 3,
+    // slice backward: 8.33 -> 8.01 ms at G = 256, 30.5 -> 29.8 at G = 1024);
+    // with bf16 dots they are loaded in the tile's own body (prefetched,
+    // the G = 1024 slice backward took 5 % longer)
+    constexpr bool PF = GModes<DK>::V == MMA_X6;
+    float xA[NB][16], xB[NB][16], fA[NB][16], fB[NB][16], sA[3], sB[3];
+    auto load = [&](float (&xn)[NB][16], float (&fn)[NB][16], float (&sn)[3], int t) {
       const int64_t p0 = (int64_t)t * kTile;
       ld_rows<T, NB, FAST>(xn, rows_rsrc(x_b, x_sn, x_w, p0, N), vrx, D, h);
       ld_rows<T, NB, FAST>(fn, rows_rsrc(f_b, f_sn, f_w, p0, N), vrf, DV, h);
+      if constexpr (PF) {
+        sn[0] = ld_pt(pts_rsrc(sm, p0, N), c);
+        sn[1] = ld_pt(pts_rsrc(slsum, p0, N), c);
+        sn[2] = ld_pt(pts_rsrc(sdel, p0, N), c);
+      }
     };
-    auto body = [&](const float (&xf)[NB][16], const float (&ff)[NB][16], int t, auto par) {
+    auto body = [&](const float (&xf)[NB][16], const float (&ff)[NB][16], const float (&sv)[3],
+                    int t, auto par) {
       const int64_t p0 = (int64_t)t * kTile;
       const bool pv = p0 + c < N;
-      const float m2 = ld_pt(pts_rsrc(sm, p0, N), c) * kLog2e;
-      const float l = ld_pt(pts_rsrc(slsum, p0, N), c);
-      const float delta = ld_pt(pts_rsrc(sdel, p0, N), c);
+      const float m2 = (PF ? sv[0] : ld_pt(pts_rsrc(sm, p0, N), c)) * kLog2e;
+      const float l = PF ? sv[1] : ld_pt(pts_rsrc(slsum, p0, N), c);
+      const float delta = PF ? sv[2] : ld_pt(pts_rsrc(sdel, p0, N), c);
       Frag<ML> xq[NB];
 #pragma unroll
       for (int k = 0; k < NB; ++k) prep<ML>(xq[k], xf[k]);
@@ -827,7 +848,7 @@ __global__ __launch_bounds__(256, NB == 1 && SLICE ? 3 : gp_waves(NB)) void k_gp
       for (int j = 0; j < 16; ++j) s += aT[j];
       dbacc = fmaf(s, sg, dbacc);
     };
-    FS_TILE_LOOP(load, body, false, FS_ARGS2(xA, fA), FS_ARGS2(xB, fB))
+    FS_TILE_LOOP(load, body, false, FS_ARGS3(xA, fA, sA), FS_ARGS3(xB, fB, sB))
   };
   if (fast) run(std::true_type()); else run(std::false_type());
   const int gg = 32 * gb + c;

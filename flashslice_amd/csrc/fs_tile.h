@@ -296,5 +296,6 @@ __device__ __forceinline__ void balance_prio(int t, int pid, int ntiles, int P) 
     }                                                                                     \
   }
 #define FS_ARGS2(X, Y) X, Y
+#define FS_ARGS3(X, Y, Z) X, Y, Z
 
 }  // namespace fs
