@@ -234,17 +234,29 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_stats(Args a) {
   };
   int g = 0;
   stage(0, 0);
+  // with the logits' operands split (the fp32-accurate levels) a tile's
+  // rows are loaded one tile ahead, right after the previous tile's were
+  // split (the slot blocks' staging waits absorb the load; config 3, G =
+  // 256: statistics and deslice 5 % faster); with bf16 dots the registers
+  // that takes would cost a wave per SIMD, and the rows are loaded at the
+  // tile's start
+  constexpr bool PF = ML == MMA_X6;
+  const int64_t pstep = (int64_t)kWavesPerBlock * gridDim.x * kTile;
+  float xf[NB][16];
+  if constexpr (PF)
+    gp_rows<T, NB>(xf, rows_rsrc(x_b, x_sn, x_w, (int64_t)(kWavesPerBlock * blockIdx.x + wid) * kTile, N),
+                   x_row, fast, D, h);
   __syncthreads();
   for (int it = 0;; ++it) {
     const int tb = kWavesPerBlock * (blockIdx.x + it * gridDim.x);
     if (tb >= ntiles_) break;
     const int64_t p0 = (int64_t)(tb + wid) * kTile;
     const bool more = tb + kWavesPerBlock * (int)gridDim.x < ntiles_;
-    float xf[NB][16];
-    gp_rows<T, NB>(xf, rows_rsrc(x_b, x_sn, x_w, p0, N), x_row, fast, D, h);
+    if constexpr (!PF) gp_rows<T, NB>(xf, rows_rsrc(x_b, x_sn, x_w, p0, N), x_row, fast, D, h);
     Frag<ML> xq[NB];
 #pragma unroll
     for (int k = 0; k < NB; ++k) prep<ML>(xq[k], xf[k]);
+    if constexpr (PF) gp_rows<T, NB>(xf, rows_rsrc(x_b, x_sn, x_w, p0 + pstep, N), x_row, fast, D, h);
     float m = -INFINITY, l = 0.f, mc = 0.f;
     for (int s = 0; s < nstage; ++s, ++g) {
       if (s + 1 < nstage || more) stage((g + 1) & 1, (s + 1) % nstage);
@@ -321,6 +333,16 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_deslice(Args a) {
   };
   int g = 0;
   stage(0, 0);
+  // a tile's rows (and saved row max) one tile ahead where the logits'
+  // operands are split, as in the statistics pass
+  constexpr bool PF = ML == MMA_X6;
+  const int64_t pstep = (int64_t)kWavesPerBlock * gridDim.x * kTile;
+  float xf[NB][16], mn = 0.f;
+  if constexpr (PF) {
+    const int64_t pf = (int64_t)(kWavesPerBlock * blockIdx.x + wid) * kTile;
+    gp_rows<T, NB>(xf, rows_rsrc(x_b, x_sn, x_w, pf, N), x_row, fast, D, h);
+    if (!ONLINE) mn = ld_pt(pts_rsrc(sin_m, pf, N), c);
+  }
   __syncthreads();
   for (int it = 0;; ++it) {
     const int tb = kWavesPerBlock * (blockIdx.x + it * gridDim.x);
@@ -328,13 +350,19 @@ __global__ __launch_bounds__(256, gp_waves(NB)) void k_gp_deslice(Args a) {
     const int64_t p0 = (int64_t)(tb + wid) * kTile;
     const bool pv = p0 + c < N;
     const bool more = tb + kWavesPerBlock * (int)gridDim.x < ntiles_;
-    float xf[NB][16];
-    gp_rows<T, NB>(xf, rows_rsrc(x_b, x_sn, x_w, p0, N), x_row, fast, D, h);
+    if constexpr (!PF) {
+      gp_rows<T, NB>(xf, rows_rsrc(x_b, x_sn, x_w, p0, N), x_row, fast, D, h);
+      if (!ONLINE) mn = ld_pt(pts_rsrc(sin_m, p0, N), c);
+    }
     Frag<ML> xq[NB];
 #pragma unroll
     for (int k = 0; k < NB; ++k) prep<ML>(xq[k], xf[k]);
     float m2 = -INFINITY, l = 0.f, lown = 0.f;
-    if (!ONLINE) m2 = ld_pt(pts_rsrc(sin_m, p0, N), c) * kLog2e;
+    if (!ONLINE) m2 = mn * kLog2e;
+    if constexpr (PF) {
+      gp_rows<T, NB>(xf, rows_rsrc(x_b, x_sn, x_w, p0 + pstep, N), x_row, fast, D, h);
+      if (!ONLINE) mn = ld_pt(pts_rsrc(sin_m, p0 + pstep, N), c);
+    }
     f32x16 acc[NB];
 #pragma unroll
     for (int k = 0; k < NB; ++k) acc[k] = zero16();
