@@ -973,11 +973,26 @@ __global__ __launch_bounds__(256, (NGB * NDB * NVB == 1) ? 2 : 1) void k_fused_t
   FS_SLICE(dx, a.o1, a.s1b, a.s1n, a.s1h, D)
   FS_SLICE(df, a.o2, a.s2b, a.s2n, a.s2h, DV)
   (void)dx_row; (void)df_row;
-  uint32_t vcx[NDB], vcf[NVB];
+  // the store offsets of dx and dfx: held across the tile loop at one block
+  // of 32 on every axis; formed at each store for the wider shapes, whose
+  // 512 registers are full (held, three of them were spilled and their
+  // reloads drained the next tile's fx / d_out loads before dx's stores)
+  constexpr bool RM = NGB * NDB * NVB > 1;
+  uint32_t vcx0[NDB], vcf0[NVB];
 #pragma unroll
-  for (int db = 0; db < NDB; ++db) vcx[db] = col_off<T>(db, D, dx_sn, c, h);
+  for (int db = 0; db < NDB; ++db) vcx0[db] = col_off<T>(db, D, dx_sn, c, h);
 #pragma unroll
-  for (int vb = 0; vb < NVB; ++vb) vcf[vb] = col_off<T>(vb, DV, df_sn, c, h);
+  for (int vb = 0; vb < NVB; ++vb) vcf0[vb] = col_off<T>(vb, DV, df_sn, c, h);
+  auto store_offs = [&](uint32_t* vc, const uint32_t* held, int nb, int C, int64_t snb) {
+    if constexpr (RM) {
+      const int l = lane_here();
+#pragma unroll
+      for (int k = 0; k < nb; ++k) vc[k] = col_off<T>(k, C, snb, l & 31, l >> 5);
+    } else {
+#pragma unroll
+      for (int k = 0; k < nb; ++k) vc[k] = held[k];
+    }
+  };
   auto run = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
     const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
@@ -1088,6 +1103,8 @@ __global__ __launch_bounds__(256, (NGB * NDB * NVB == 1) ? 2 : 1) void k_fused_t
           }
           // no dfx wanted (a.o2 null): an empty range drops every store
           const Rsrc rdf = rows_rsrc_sel(df_b, df_sn, df_w, p0, a.o2 ? N : 0);
+          uint32_t vcf[NVB];
+          store_offs(vcf, vcf0, NVB, DV, df_sn);
 #pragma unroll
           for (int vb = 0; vb < NVB; ++vb) st_cols<T>(rdf, vcf[vb], (uint32_t)df_sn, o[vb]);
         }
@@ -1097,6 +1114,8 @@ __global__ __launch_bounds__(256, (NGB * NDB * NVB == 1) ? 2 : 1) void k_fused_t
         // dW and the next tile's logits still cover the loads' latency
         load_f(t + a.P);
         load_g(t + a.P);
+        uint32_t vcx[NDB];
+        store_offs(vcx, vcx0, NDB, D, dx_sn);
         FS_DX_DW(om, qWc, sg)
       }
     };

@@ -217,6 +217,18 @@ __device__ __forceinline__ void ld_cols_here(float (&f)[16], Rsrc r, uint32_t vc
   for (int j = 0; j < 16; ++j) f[j] = Buf<T>::ld1(r, vc + (uint32_t)tile_row(j) * snb);
 }
 
+// This lane's index in its wave, formed anew at each use: the asm is
+// volatile, so the compiler neither hoists it out of a loop nor shares it
+// between uses. Offsets derived from it are rematerialised at their use
+// instead of being held across a tile loop, which a kernel at its register
+// limit would spill (each reload from scratch waits for every load in flight,
+// the next tile's prefetch included).
+__device__ __forceinline__ int lane_here() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 // Store a [column-outer, point-inner] fragment (the transposed twin of
 // ld_cols): every store instruction writes two whole 32-column row segments.
 template <typename T>
