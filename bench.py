@@ -923,7 +923,8 @@ def main():
     total_bytes = sum(bytes_[n] for n in OPS)
     total_flops = sum(flops[n] for n in OPS)
     step_ach = total_bytes / (ms_step * 1e-3) / 1e9
-    traffic_name = a.workload + ("-tied" if a.tied else "")
+    # counted on fp32 point tensors: a bf16 line has its own file or none
+    traffic_name = a.workload + ("-bf16" if a.dot == "bf16" else "") + ("-tied" if a.tied else "")
     traffic = measured_traffic(traffic_name)
 
     cpu = None
