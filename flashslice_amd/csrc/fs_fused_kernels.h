@@ -438,6 +438,33 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
   if (fast) run(std::true_type()); else run(std::false_type());
 }
 
+// Store offsets (col_off) of NB column blocks of a point output, indexed
+// like an array at each store: held in registers, formed before the tile
+// loop, at one block of 32 on every axis; formed anew at each store from the
+// lane index (lane_here) where RM is set, for the wider shapes, whose
+// registers are full: held there, they were spilled, and each reload from
+// scratch waits for every load in flight, the next tile's prefetch included.
+template <typename T, bool RM, int NB>
+struct StoreOffs {
+  uint32_t held[NB];
+  int C;
+  int64_t snb;
+  __device__ __forceinline__ StoreOffs(int C_, int64_t snb_, int c, int h) : C(C_), snb(snb_) {
+    if constexpr (!RM) {
+#pragma unroll
+      for (int k = 0; k < NB; ++k) held[k] = col_off<T>(k, C, snb, c, h);
+    }
+  }
+  __device__ __forceinline__ uint32_t operator[](int k) const {
+    if constexpr (RM) {
+      const int l = lane_here();
+      return col_off<T>(k, C, snb, l & 31, l >> 5);
+    } else {
+      return held[k];
+    }
+  }
+};
+
 // dx = Lb (W / tau) and dW += Lb^T x, db += sum_n Lb (scaled by 1 / tau
 // when the partials are written) for the two backward kernels: `om` holds
 // Lb ([point-outer, slot-inner]); qWc the ready fragments of W / tau as
@@ -550,11 +577,9 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_slice
   FS_SLICE(dx, a.o1, a.s1b, a.s1n, a.s1h, D)
   FS_SLICE(df, a.o2, a.s2b, a.s2n, a.s2h, DV)
   (void)dx_row; (void)df_row;
-  uint32_t vcx[NDB], vcf[NVB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) vcx[db] = col_off<T>(db, D, dx_sn, c, h);
-#pragma unroll
-  for (int vb = 0; vb < NVB; ++vb) vcf[vb] = col_off<T>(vb, DV, df_sn, c, h);
+  constexpr bool RM = NGB * NDB * NVB > 1;
+  const StoreOffs<T, RM, NDB> vcx(D, dx_sn, c, h);
+  const StoreOffs<T, RM, NVB> vcf(DV, df_sn, c, h);
   auto run = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
     const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
@@ -745,9 +770,7 @@ __global__ __launch_bounds__(256, fused_waves(NGB, NDB, NVB)) void k_fused_desli
   FS_SLICE(g, a.f, a.sfb, a.sfn, a.sfh, DV)
   FS_SLICE(dx, a.o1, a.s1b, a.s1n, a.s1h, D)
   (void)dx_row;
-  uint32_t vcx[NDB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) vcx[db] = col_off<T>(db, D, dx_sn, c, h);
+  const StoreOffs<T, (NGB * NDB * NVB > 1), NDB> vcx(D, dx_sn, c, h);
   auto run = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
     const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
@@ -973,26 +996,9 @@ __global__ __launch_bounds__(256, (NGB * NDB * NVB == 1) ? 2 : 1) void k_fused_t
   FS_SLICE(dx, a.o1, a.s1b, a.s1n, a.s1h, D)
   FS_SLICE(df, a.o2, a.s2b, a.s2n, a.s2h, DV)
   (void)dx_row; (void)df_row;
-  // the store offsets of dx and dfx: held across the tile loop at one block
-  // of 32 on every axis; formed at each store for the wider shapes, whose
-  // 512 registers are full (held, three of them were spilled and their
-  // reloads drained the next tile's fx / d_out loads before dx's stores)
   constexpr bool RM = NGB * NDB * NVB > 1;
-  uint32_t vcx0[NDB], vcf0[NVB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) vcx0[db] = col_off<T>(db, D, dx_sn, c, h);
-#pragma unroll
-  for (int vb = 0; vb < NVB; ++vb) vcf0[vb] = col_off<T>(vb, DV, df_sn, c, h);
-  auto store_offs = [&](uint32_t* vc, const uint32_t* held, int nb, int C, int64_t snb) {
-    if constexpr (RM) {
-      const int l = lane_here();
-#pragma unroll
-      for (int k = 0; k < nb; ++k) vc[k] = col_off<T>(k, C, snb, l & 31, l >> 5);
-    } else {
-#pragma unroll
-      for (int k = 0; k < nb; ++k) vc[k] = held[k];
-    }
-  };
+  const StoreOffs<T, RM, NDB> vcx(D, dx_sn, c, h);
+  const StoreOffs<T, RM, NVB> vcf(DV, df_sn, c, h);
   auto run = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
     const uint32_t vrx = FAST ? x_row + 4 * h * (uint32_t)sizeof(T) : x_row;
@@ -1103,8 +1109,6 @@ __global__ __launch_bounds__(256, (NGB * NDB * NVB == 1) ? 2 : 1) void k_fused_t
           }
           // no dfx wanted (a.o2 null): an empty range drops every store
           const Rsrc rdf = rows_rsrc_sel(df_b, df_sn, df_w, p0, a.o2 ? N : 0);
-          uint32_t vcf[NVB];
-          store_offs(vcf, vcf0, NVB, DV, df_sn);
 #pragma unroll
           for (int vb = 0; vb < NVB; ++vb) st_cols<T>(rdf, vcf[vb], (uint32_t)df_sn, o[vb]);
         }
@@ -1114,8 +1118,6 @@ __global__ __launch_bounds__(256, (NGB * NDB * NVB == 1) ? 2 : 1) void k_fused_t
         // dW and the next tile's logits still cover the loads' latency
         load_f(t + a.P);
         load_g(t + a.P);
-        uint32_t vcx[NDB];
-        store_offs(vcx, vcx0, NDB, D, dx_sn);
         FS_DX_DW(om, qWc, sg)
       }
     };
