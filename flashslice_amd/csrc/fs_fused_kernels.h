@@ -216,7 +216,13 @@ __global__ __launch_bounds__(256, slice_fwd_waves(NGB, NDB, NVB)) void k_fused_s
       ld_rows<T, NDB, FAST>(xn, rows_rsrc(x_b, x_sn, x_w, p0, N), vrx, D, h);
       const Rsrc rf = rows_rsrc(f_b, f_sn, f_w, p0, N);
 #pragma unroll
-      for (int vb = 0; vb < NVB; ++vb) ld_cols<T>(fn[vb], rf, vcf[vb], (uint32_t)f_sn);
+      for (int vb = 0; vb < NVB; ++vb) {
+        // with per-element x loads (unaligned rows, or a width not a multiple
+        // of 32) the sixteen hoisted fx row offsets would be spilled, and each
+        // reload from scratch would wait for every load in flight
+        if constexpr (FAST) ld_cols<T>(fn[vb], rf, vcf[vb], (uint32_t)f_sn);
+        else ld_cols_here<T>(fn[vb], rf, vcf[vb], (uint32_t)f_sn);
+      }
     };
     // the wave's first two tiles are in flight while the block stages W
     load(xA, fA, pid);
